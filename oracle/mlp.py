@@ -1,0 +1,64 @@
+"""fp32 SwiGLU MLP formula (oracle; test infrastructure only).
+
+The reference's CPU path for the MLP is the fp32 torch expression
+``(silu(a @ G.T) * (a @ U.T)) @ D.T`` (``scripts/ci/mlp-sweep.py:121-126``); its single-device
+module applies the same order -- gate linear with SiLU, up linear, multiply, down linear
+(``docker/qwen-c2-graft/graft/mlp.py:402-423``) -- and the decoder layer adds the residual stream
+afterwards (``docker/qwen-c2-graft/graft/layer.py:352-357``).  This module restates that formula in
+numpy float32 (BLAS sgemm accumulates in fp32), plus the same formula in torch for the CPU
+baseline timing.
+"""
+import numpy as np
+
+
+def silu(v):
+    """SiLU in the dtype of ``v``: ``v / (1 + exp(-v))``."""
+    v = np.asarray(v)
+    one = v.dtype.type(1)
+    return v / (one + np.exp(-v))
+
+
+def swiglu(x, wg, wu, wd, residual=None):
+    """``residual + down(silu(gate(x)) * up(x))`` in float32.
+
+    x: [M, H]; wg, wu: [I, H] (out, in); wd: [H, I]; residual: [M, H] or None.
+    Follows ``scripts/ci/mlp-sweep.py:121-126`` and ``layer.py:357``.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    g = x @ np.asarray(wg, dtype=np.float32).T
+    u = x @ np.asarray(wu, dtype=np.float32).T
+    h = silu(g) * u
+    y = h @ np.asarray(wd, dtype=np.float32).T
+    if residual is not None:
+        y = y + np.asarray(residual, dtype=np.float32)
+    return y.astype(np.float32)
+
+
+def swiglu_hidden(x, wg, wu):
+    """The intermediate ``silu(gate(x)) * up(x)`` in float32 (``fused_1d.py:10-22`` computes it on
+    device as the gate/up projection output)."""
+    x = np.asarray(x, dtype=np.float32)
+    g = x @ np.asarray(wg, dtype=np.float32).T
+    u = x @ np.asarray(wu, dtype=np.float32).T
+    return (silu(g) * u).astype(np.float32)
+
+
+def swiglu_torch(x, wg, wu, wd, residual=None):
+    """The same formula with torch CPU tensors (float32), exactly the reference's expression
+    ``(torch.nn.functional.silu(a @ G.T) * (a @ U.T)) @ D.T`` (``scripts/ci/mlp-sweep.py:126``)."""
+    import torch
+
+    y = (torch.nn.functional.silu(x @ wg.T) * (x @ wu.T)) @ wd.T
+    if residual is not None:
+        y = y + residual
+    return y
+
+
+def tolerance_ok(actual, expected, rel=1e-2):
+    """Parity bar: ``max|actual - expected| <= rel * RMS(expected)``.  Returns (ok, err, bound)."""
+    actual = np.asarray(actual, dtype=np.float64)
+    expected = np.asarray(expected, dtype=np.float64)
+    rms = float(np.sqrt(np.mean(expected * expected)))
+    err = float(np.max(np.abs(actual - expected))) if expected.size else 0.0
+    bound = rel * rms
+    return err <= bound, err, bound

@@ -1,0 +1,27 @@
+"""MI355X (gfx950) fused Qwen3 SwiGLU MLP: ``out = residual + down(silu(gate(x)) * up(x))``.
+
+Host code for ``libqwen_mlp.so`` (hand-written HIP kernels behind the C ABI in
+``include/qwen_mlp.h``).  The public surface mirrors the reference module
+``docker/qwen-c2-graft/graft/mlp.py``: ``Qwen36MLP``, ``MLPWeights``, ``load_mlp_weights``.
+"""
+from ._lib import FMT_BF16, FMT_BFP8, LIB_PATH, QmlpError, lib
+from .mlp import (
+    MLPWeights,
+    PackedWeight,
+    Qwen36MLP,
+    dequantize,
+    load_mlp_weights,
+    mlp_forward,
+    new_workspace,
+    pack_canonical_bfp8,
+    pack_weight,
+    quantize_bfp8,
+    unpack_bfp8,
+    workspace_bytes,
+)
+
+__all__ = [
+    "FMT_BF16", "FMT_BFP8", "LIB_PATH", "QmlpError", "lib", "MLPWeights", "PackedWeight", "Qwen36MLP",
+    "dequantize", "load_mlp_weights", "mlp_forward", "new_workspace", "pack_canonical_bfp8", "pack_weight",
+    "quantize_bfp8", "unpack_bfp8", "workspace_bytes",
+]

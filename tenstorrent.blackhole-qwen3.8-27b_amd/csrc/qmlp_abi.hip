@@ -1,0 +1,234 @@
+// qmlp_abi.hip -- the extern "C" boundary of libqwen_mlp.so (declared in include/qwen_mlp.h):
+// argument validation, error reporting, workspace layout and dispatch.  No call allocates.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "../../include/qwen_mlp.h"
+#include "qmlp_common.h"
+#include "qmlp_internal.h"
+
+namespace qmlp {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(QMLP_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return 0;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+WsLayout ws_layout(int M, int H, int I, int fmt) {
+  WsLayout L{};
+  size_t off = 0;
+  L.counters_gu = off;
+  off = align256(off + (size_t)(I / kTileRows) * 4);
+  L.counters_d = off;
+  off = align256(off + (size_t)(H / kTileRows) * 4);
+  L.tx = off;
+  off = align256(off + (size_t)M * 4);
+  L.th = off;
+  off = align256(off + (size_t)M * 4);
+  L.x16 = off;
+  off = align256(off + (fmt == QMLP_FMT_BFP8 ? (size_t)M * H * 2 : 0));
+  L.h = off;
+  off = align256(off + (size_t)M * I * 2);
+  L.part_gu = off;  // 2 slots per workgroup, 2 matrices x 2 column tiles x 64 lanes x 16 B
+  off = align256(off + (size_t)2 * kMaxWorkgroups * (2 * 2 * 64 * 16));
+  L.part_d = off;
+  off = align256(off + (size_t)2 * kMaxWorkgroups * (1 * 2 * 64 * 16));
+  L.total = off;
+  return L;
+}
+
+struct DeviceInfo {
+  int ok;  // 1 = gfx950, -1 = unusable
+  int num_cus;
+};
+
+static DeviceInfo device_info(int dev) {
+  static std::mutex mu;
+  static DeviceInfo cache[64] = {};
+  if (dev < 0 || dev >= 64) return DeviceInfo{-1, 0};
+  std::lock_guard<std::mutex> g(mu);
+  if (cache[dev].ok == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+      cache[dev] = DeviceInfo{-1, 0};
+    } else {
+      const bool gfx950 = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+      cache[dev] = DeviceInfo{gfx950 ? 1 : -1, prop.multiProcessorCount};
+    }
+  }
+  return cache[dev];
+}
+
+static int current_device_info(DeviceInfo* out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(QMLP_E_DEVICE, "no HIP device");
+  *out = device_info(dev);
+  if (out->ok != 1) return set_error(QMLP_E_DEVICE, "device %d is not a gfx950 (MI355X) GPU", dev);
+  return 0;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static bool shape_ok(int rows, int cols) {
+  return rows > 0 && cols > 0 && rows % kTileRows == 0 && cols % kSuperK == 0 && rows <= (1 << 20) &&
+         cols <= (1 << 20);
+}
+
+}  // namespace qmlp
+
+using namespace qmlp;
+
+extern "C" {
+
+const char* qmlp_last_error(void) { return g_err; }
+
+const char* qmlp_version(void) { return "qwen_mlp 0.1 gfx950"; }
+
+size_t qmlp_packed_bytes(int rows, int cols, int fmt) {
+  if (!shape_ok(rows, cols) || (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8)) return 0;
+  return packed_total(rows, cols, fmt);
+}
+
+int qmlp_quantize_bfp8(const void* w_bf16, int rows, int cols, void* q, void* e8, uint32_t* bad_groups,
+                       qmlp_stream_t stream) {
+  if (!w_bf16 || !q || !e8) return set_error(QMLP_E_NULL, "qmlp_quantize_bfp8: null pointer");
+  if (rows <= 0 || cols <= 0 || cols % 16) return set_error(QMLP_E_SHAPE, "qmlp_quantize_bfp8: bad shape %dx%d", rows, cols);
+  if (!aligned16(w_bf16) || !aligned16(q)) return set_error(QMLP_E_ALIGN, "qmlp_quantize_bfp8: misaligned pointer");
+  DeviceInfo di;
+  if (int rc = current_device_info(&di)) return rc;
+  return launch_quantize(w_bf16, rows, cols, q, e8, bad_groups, (hipStream_t)stream);
+}
+
+int qmlp_pack(const void* src0, const void* src1, int rows, int cols, int fmt, void* packed, size_t packed_bytes,
+              qmlp_stream_t stream) {
+  if (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8) return set_error(QMLP_E_FORMAT, "qmlp_pack: unknown format %d", fmt);
+  if (!src0 || !packed || (fmt == QMLP_FMT_BFP8 && !src1)) return set_error(QMLP_E_NULL, "qmlp_pack: null pointer");
+  if (!shape_ok(rows, cols))
+    return set_error(QMLP_E_SHAPE, "qmlp_pack: rows must be a multiple of 16 and cols of 256 (%dx%d)", rows, cols);
+  if (!aligned16(src0) || !aligned16(packed)) return set_error(QMLP_E_ALIGN, "qmlp_pack: misaligned pointer");
+  if (packed_bytes < packed_total(rows, cols, fmt))
+    return set_error(QMLP_E_WORKSPACE, "qmlp_pack: packed buffer holds %zu bytes, needs %zu", packed_bytes,
+                     packed_total(rows, cols, fmt));
+  DeviceInfo di;
+  if (int rc = current_device_info(&di)) return rc;
+  return launch_pack(src0, src1, rows, cols, fmt, packed, (hipStream_t)stream);
+}
+
+int qmlp_packed_info(const void* packed, int rows, int cols, int fmt, double* max_row_norm, uint32_t* flushed_groups,
+                     qmlp_stream_t stream) {
+  if (!packed) return set_error(QMLP_E_NULL, "qmlp_packed_info: null pointer");
+  if (!shape_ok(rows, cols) || (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8))
+    return set_error(QMLP_E_SHAPE, "qmlp_packed_info: bad shape/format");
+  DeviceInfo di;
+  if (int rc = current_device_info(&di)) return rc;
+  Trailer t;
+  const uint8_t* src = (const uint8_t*)packed + trailer_offset(rows, cols, fmt);
+  if (hipMemcpyAsync(&t, src, sizeof(t), hipMemcpyDeviceToHost, (hipStream_t)stream) != hipSuccess ||
+      hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
+    return set_error(QMLP_E_LAUNCH, "qmlp_packed_info: copy failed");
+  if (t.magic != kTrailerMagic) return set_error(QMLP_E_FORMAT, "qmlp_packed_info: buffer was not packed by qmlp_pack");
+  double n;
+  memcpy(&n, &t.max_row_norm_bits, sizeof(n));
+  if (max_row_norm) *max_row_norm = n;
+  if (flushed_groups) *flushed_groups = t.flushed_groups;
+  return 0;
+}
+
+int qmlp_unpack_bfp8(const void* packed, int rows, int cols, void* q, void* e8, qmlp_stream_t stream) {
+  if (!packed || !q || !e8) return set_error(QMLP_E_NULL, "qmlp_unpack_bfp8: null pointer");
+  if (!shape_ok(rows, cols)) return set_error(QMLP_E_SHAPE, "qmlp_unpack_bfp8: bad shape %dx%d", rows, cols);
+  if (!aligned16(packed) || !aligned16(q)) return set_error(QMLP_E_ALIGN, "qmlp_unpack_bfp8: misaligned pointer");
+  DeviceInfo di;
+  if (int rc = current_device_info(&di)) return rc;
+  return launch_unpack_bfp8(packed, rows, cols, q, e8, (hipStream_t)stream);
+}
+
+int qmlp_dequant_packed(const void* packed, int rows, int cols, int fmt, float* out, qmlp_stream_t stream) {
+  if (!packed || !out) return set_error(QMLP_E_NULL, "qmlp_dequant_packed: null pointer");
+  if (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8) return set_error(QMLP_E_FORMAT, "qmlp_dequant_packed: unknown format");
+  if (!shape_ok(rows, cols)) return set_error(QMLP_E_SHAPE, "qmlp_dequant_packed: bad shape %dx%d", rows, cols);
+  if (!aligned16(packed) || !aligned16(out)) return set_error(QMLP_E_ALIGN, "qmlp_dequant_packed: misaligned pointer");
+  DeviceInfo di;
+  if (int rc = current_device_info(&di)) return rc;
+  return launch_dequant(packed, rows, cols, fmt, out, (hipStream_t)stream);
+}
+
+size_t qmlp_workspace_bytes(int M, int H, int I, int fmt) {
+  if (M < 1 || M > 65536 || !shape_ok(16, H) || !shape_ok(16, I) || (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8))
+    return 0;
+  return ws_layout(M, H, I, fmt).total;
+}
+
+int qmlp_workspace_init(void* ws, size_t ws_bytes, qmlp_stream_t stream) {
+  if (!ws) return set_error(QMLP_E_NULL, "qmlp_workspace_init: null pointer");
+  if (!aligned16(ws)) return set_error(QMLP_E_ALIGN, "qmlp_workspace_init: misaligned pointer");
+  DeviceInfo di;
+  if (int rc = current_device_info(&di)) return rc;
+  return launch_fill_zero(ws, ws_bytes, (hipStream_t)stream);
+}
+
+int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* wd, const void* residual, void* out,
+                    void* ws, size_t ws_bytes, int M, int H, int I, int fmt, int flags, qmlp_stream_t stream) {
+  if (!x || !wg || !wu || !wd || !out || !ws) return set_error(QMLP_E_NULL, "qmlp_forward: null pointer");
+  if (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8) return set_error(QMLP_E_FORMAT, "qmlp_forward: unknown format %d", fmt);
+  if (flags & ~(QMLP_OUT_F32 | QMLP_RESIDUAL_F32)) return set_error(QMLP_E_FORMAT, "qmlp_forward: unknown flags 0x%x", flags);
+  if (M < 1 || M > 65536) return set_error(QMLP_E_SHAPE, "qmlp_forward: M=%d out of range [1, 65536]", M);
+  if (!shape_ok(16, H) || !shape_ok(16, I))
+    return set_error(QMLP_E_SHAPE, "qmlp_forward: H=%d and I=%d must be positive multiples of 256", H, I);
+  if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(ws) ||
+      (residual && !aligned16(residual)))
+    return set_error(QMLP_E_ALIGN, "qmlp_forward: every pointer must be 16-byte aligned");
+  const size_t xbytes = (size_t)M * H * 2, obytes = (size_t)M * H * ((flags & QMLP_OUT_F32) ? 4 : 2);
+  const uintptr_t xb = (uintptr_t)x, ob = (uintptr_t)out;
+  if (xb < ob + obytes && ob < xb + xbytes) return set_error(QMLP_E_SHAPE, "qmlp_forward: out must not overlap x");
+  if (residual && residual != out) {
+    const size_t rbytes = (size_t)M * H * ((flags & QMLP_RESIDUAL_F32) ? 4 : 2);
+    const uintptr_t rb = (uintptr_t)residual;
+    if (rb < ob + obytes && ob < rb + rbytes)
+      return set_error(QMLP_E_SHAPE, "qmlp_forward: out may equal residual but must not partially overlap it");
+  }
+  if (residual == out && residual && ((flags & QMLP_OUT_F32) != 0) != ((flags & QMLP_RESIDUAL_F32) != 0))
+    return set_error(QMLP_E_SHAPE, "qmlp_forward: an in-place residual needs the same dtype as out");
+  const WsLayout L = ws_layout(M, H, I, fmt);
+  if (ws_bytes < L.total)
+    return set_error(QMLP_E_WORKSPACE, "qmlp_forward: workspace holds %zu bytes, needs %zu", ws_bytes, L.total);
+  DeviceInfo di;
+  if (int rc = current_device_info(&di)) return rc;
+  ForwardArgs a{x, (const uint8_t*)wg, (const uint8_t*)wu, (const uint8_t*)wd, residual, out, (uint8_t*)ws,
+                M, H, I, fmt, (flags & QMLP_OUT_F32) ? 1 : 0, (flags & QMLP_RESIDUAL_F32) ? 1 : 0};
+  return launch_forward_skinny(a, di.num_cus, (hipStream_t)stream);
+}
+
+int qmlp_forward(const void* x, const void* wg, const void* wu, const void* wd, const void* residual, void* out,
+                 void* ws, size_t ws_bytes, int M, int H, int I, int fmt, qmlp_stream_t stream) {
+  return qmlp_forward_ex(x, wg, wu, wd, residual, out, ws, ws_bytes, M, H, I, fmt, 0, stream);
+}
+
+int qmlp_plan_skinny(int rows, int K, int M, int num_cus, int* out4) {
+  if (!out4) return set_error(QMLP_E_NULL, "qmlp_plan_skinny: null pointer");
+  SkinnyPlan p;
+  if (plan_skinny(rows, K, M, num_cus, &p)) return set_error(QMLP_E_SHAPE, "qmlp_plan_skinny: bad shape %dx%d", rows, K);
+  out4[0] = p.P;
+  out4[1] = p.NW;
+  out4[2] = p.T * p.C;
+  out4[3] = p.aligned;
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,122 @@
+// qmlp_common.h -- layout constants and device helpers shared by the gfx950 kernels.
+//
+// Packed ("tiled") weight layout, one matrix W[rows, K] (rows = output features):
+//   * 16-row tiles x 256-K superblocks, block index u = tile * (K/256) + superblock (tile-major);
+//   * bfp8 block (4352 B): 4 K-steps x 1024 B of excess-128 mantissas, then 256 B of exponents.
+//     In K-step j, lane l (row r = l%16, quarter q = l/16) owns bytes [j*1024 + 16l, +16): the
+//     mantissas u = q8 + 128 of K = 256*sb + 64*j + 16*q + (0..15) of row r (one 16-value group).
+//     Exponent dword of lane l (bytes 4096 + 4l): byte j = E5 << 2, the high byte of the IEEE half
+//     2^(E5-15) that scales that group (0 = all-zero group).
+//   * bf16 block (8192 B): per K-step two 1 KB halves; lane l owns values 0..7 of its 16 at
+//     j*2048 + 16l and values 8..15 at j*2048 + 1024 + 16l.
+//   * after the blocks: int32 rowexp[rows] (true weight = (u-128) * 2^(E5-15) * 2^rowexp), then a
+//     256-byte trailer {double max_row_norm; uint32 flushed_groups; uint32 magic}.
+// One 16x16x32 matrix-core product consumes, per lane, 8 consecutive K values of one weight row
+// (A operand) and the same 8 K values of one token row (B operand); the K order inside a lane is
+// free as long as A and B agree, which the layout above guarantees.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qmlp {
+
+constexpr int kTileRows = 16;
+constexpr int kSuperK = 256;
+constexpr int kSteps = 4;
+constexpr int kBfp8Block = kSteps * 1024 + 256;  // 4352
+constexpr int kBf16Block = kSteps * 2048;        // 8192
+constexpr int kTrailer = 256;
+constexpr uint32_t kTrailerMagic = 0x514d4c50u;  // "PLMQ"
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct Trailer {
+  unsigned long long max_row_norm_bits;  // IEEE double bits (non-negative, so integer max works)
+  uint32_t flushed_groups;
+  uint32_t magic;
+};
+
+__host__ __device__ inline size_t tiles_bytes(int rows, int cols, int fmt) {
+  return (size_t)(rows / kTileRows) * (size_t)(cols / kSuperK) * (fmt == 1 ? kBfp8Block : kBf16Block);
+}
+__host__ __device__ inline size_t rowexp_offset(int rows, int cols, int fmt) { return tiles_bytes(rows, cols, fmt); }
+__host__ __device__ inline size_t trailer_offset(int rows, int cols, int fmt) {
+  return tiles_bytes(rows, cols, fmt) + (size_t)rows * 4;
+}
+__host__ __device__ inline size_t packed_total(int rows, int cols, int fmt) {
+  return trailer_offset(rows, cols, fmt) + kTrailer;
+}
+
+// ---------------------------------------------------------------- scalar conversions
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (quiet NaN kept), the same word arithmetic as torch's cast.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t w = __float_as_uint(f);
+  if ((w & 0x7f800000u) == 0x7f800000u && (w & 0x007fffffu)) return (uint16_t)((w >> 16) | 0x40u);
+  return (uint16_t)((w + 0x7fffu + ((w >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// ---------------------------------------------------------------- memory helpers
+
+template <typename T>
+__device__ __forceinline__ T ld_stream(const T* p) {  // streamed once: do not keep in cache
+  return __builtin_nontemporal_load(p);
+}
+
+// ---------------------------------------------------------------- bfp8 in-register dequant
+//
+// Mantissa byte u (excess-128) and the byte-permute constant 0x64 form the half 0x64uu = 1024+u.
+// One packed fma  (1024+u)*s + (-1152*s) = (u-128)*s  gives the exact dequantised half for
+// s = 2^(E5-15) with E5 in [1, 20] (|value| <= 127*32, every product and sum exactly representable).
+
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+__device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// Scale pair (s, s) of K-step j from the lane's exponent dword.
+__device__ __forceinline__ f16x2 scale_pair(uint32_t edw, int j) {
+  // perm selector bytes, low to high: 0x0c (constant 0x00), j (exponent byte j of src1), 0x0c, j.
+  const uint32_t sel = 0x000c000cu | ((uint32_t)j << 24) | ((uint32_t)j << 8);
+  return as_f16x2(__builtin_amdgcn_perm(0u, edw, sel));
+}
+
+// Dequantise 4 mantissa bytes -> 4 halves (two f16x2, K order preserved).
+__device__ __forceinline__ void dq4(uint32_t w, f16x2 s, f16x2 c, f16x2& lo, f16x2& hi) {
+  const f16x2 m0 = as_f16x2(__builtin_amdgcn_perm(0x64646464u, w, 0x04010400u));
+  const f16x2 m1 = as_f16x2(__builtin_amdgcn_perm(0x64646464u, w, 0x04030402u));
+  lo = __builtin_elementwise_fma(m0, s, c);
+  hi = __builtin_elementwise_fma(m1, s, c);
+}
+
+// 16 mantissas of one lane (one K-step) -> two 8-half operands (values 0..7 and 8..15).
+__device__ __forceinline__ void dq16(u32x4 w, f16x2 s, f16x8& a0, f16x8& a1) {
+  const f16x2 c = s * f16x2{(_Float16)-1152.0f, (_Float16)-1152.0f};
+  f16x2 p0, p1, p2, p3, p4, p5, p6, p7;
+  dq4(w.x, s, c, p0, p1);
+  dq4(w.y, s, c, p2, p3);
+  dq4(w.z, s, c, p4, p5);
+  dq4(w.w, s, c, p6, p7);
+  a0 = f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+  a1 = f16x8{p4.x, p4.y, p5.x, p5.y, p6.x, p6.y, p7.x, p7.y};
+}
+
+// Logical workgroup index so that consecutive logical indices share an XCD (hardware dispatches
+// workgroup b to XCD b % 8): each XCD then streams one contiguous eighth of the weights and
+// neighbouring workgroups that share a tile exchange partial sums through the same L2.
+__device__ __forceinline__ int xcd_logical(int b, int P) {
+  if (P % 8) return b;
+  return (b % 8) * (P / 8) + b / 8;
+}
+
+}  // namespace qmlp

@@ -1,0 +1,58 @@
+// qmlp_internal.h -- host-side declarations shared by the library's translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qmlp {
+
+// Error reporting (thread-local message, set by the C ABI layer and the launchers).
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// Load-time kernels (qmlp_pack.hip).
+int launch_quantize(const void* w, int rows, int cols, void* q, void* e8, uint32_t* bad, hipStream_t s);
+int launch_pack(const void* src0, const void* src1, int rows, int cols, int fmt, void* packed, hipStream_t s);
+int launch_unpack_bfp8(const void* packed, int rows, int cols, void* q, void* e8, hipStream_t s);
+int launch_dequant(const void* packed, int rows, int cols, int fmt, float* out, hipStream_t s);
+int launch_fill_zero(void* p, size_t bytes, hipStream_t s);
+
+// Work split of one weight-streaming projection.
+struct SkinnyPlan {
+  int P;        // workgroups
+  int NW;       // waves per workgroup
+  int T;        // 16-row tiles
+  int C;        // 256-K superblocks per tile
+  int aligned;  // workgroup ranges aligned to whole tiles (no cross-workgroup partial sums)
+};
+constexpr int kMaxWorkgroups = 512;  // upper bound used to size the workspace
+constexpr int kMaxSeg = 2;            // tiles one wave may touch
+int plan_skinny(int rows, int K, int M, int num_cus, SkinnyPlan* plan);
+
+// Workspace layout for one forward call.
+struct WsLayout {
+  size_t counters_gu, counters_d;  // int32 per tile
+  size_t tx, th;                   // int32 per token
+  size_t x16;                      // f16 [M, H] (bfp8 only)
+  size_t h;                        // 16-bit [M, I]
+  size_t part_gu, part_d;          // fp32 partial-sum slots
+  size_t total;
+};
+WsLayout ws_layout(int M, int H, int I, int fmt);
+
+// Hot-path launchers.
+struct ForwardArgs {
+  const void* x;
+  const uint8_t* wg;
+  const uint8_t* wu;
+  const uint8_t* wd;
+  const void* residual;
+  void* out;
+  uint8_t* ws;
+  int M, H, I, fmt;
+  int out_f32, res_f32;  // fp32 output / fp32 residual instead of bf16
+};
+int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s);
+int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s);
+
+}  // namespace qmlp

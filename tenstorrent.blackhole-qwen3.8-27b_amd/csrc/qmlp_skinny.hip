@@ -1,0 +1,514 @@
+// qmlp_skinny.hip -- weight-streaming kernels for M <= 32 tokens (decode / speculative verify).
+//
+// Reference realisation being replaced: FusedProjection (scripts/ci/fused_1d.py:96-196) with its
+// activation multicast (fused_1d_input.cpp:1-51) and weight reader (fused_1d_weights.cpp:1-44),
+// then the widened down projection (scripts/ci/mlp_down_grid.py:4-12).  Here:
+//
+//   prep     (bfp8 only) x bf16 -> x16 = fp16(x * 2^tx[m]) with a per-token power of two that puts
+//            max|x[m]| in [2^14, 2^15), and th[m] from the Cauchy-Schwarz bound
+//            |h| <= |x_m|^2 max|Wg_n| max|Wu_n| so that h * 2^th[m] fits fp16.
+//   gate/up  one kernel streams Wg and Wu tile by tile; per 16-row tile the products of both
+//            matrices accumulate in fp32 matrix-core registers; the epilogue applies the row and
+//            token scales, h = bf16(silu(g) * u) (one rounding, as the reference's fused
+//            epilogue), and writes h (bf16, or fp16 * 2^th for bfp8).  Gate and up never leave
+//            registers.
+//   down     same kernel with one matrix over K = I; epilogue out = residual + y, written as bf16
+//            (rounded once) or fp32.
+//
+// Work split ("stream-K"): the (tile, 256-K superblock) units of a projection are divided evenly
+// over P = #CUs workgroups; a workgroup's contiguous range is divided evenly over its 8 waves at
+// stage granularity.  A wave accumulates in registers and parks its partial sums in LDS at each
+// tile boundary; after one barrier the partials of each tile are summed in wave order.  A tile
+// cut by a workgroup boundary is finished by the later of its (at most two) workgroups: partial
+// sums go through a workspace slot and a per-tile arrival counter, summed in workgroup order, so
+// results are bitwise deterministic.  Counters are reset by the finishing workgroup.
+#include "qmlp_common.h"
+#include "qmlp_internal.h"
+
+namespace qmlp {
+
+struct SkParams {
+  const uint8_t* w0;
+  const uint8_t* w1;
+  const int* rowexp0;
+  const int* rowexp1;
+  const uint16_t* B;  // [M, K] activations (bf16 or scaled fp16), row-major
+  int M, K, N, C, T, P, aligned;
+  const int* bscale;  // bfp8: B = true * 2^bscale[m]
+  const int* hscale;  // bfp8 gate/up: h16 = h * 2^hscale[m]
+  void* out;          // [M, N]: 16-bit (h, or bf16 output), or fp32 when out_f32
+  const void* residual;  // [M, N] bf16, or fp32 when res_f32; may alias out
+  int out_f32, res_f32;
+  float* partials;
+  int* counters;
+};
+
+__device__ __forceinline__ void wg_range(const SkParams& p, int w, int& a, int& b) {
+  if (p.aligned) {
+    a = (int)((long)w * p.T / p.P) * p.C;
+    b = (int)((long)(w + 1) * p.T / p.P) * p.C;
+  } else {
+    const long U = (long)p.T * p.C;
+    a = (int)((long)w * U / p.P);
+    b = (int)((long)(w + 1) * U / p.P);
+  }
+}
+
+// Workgroup whose range holds unit u: the largest w with start(w) <= u.
+__device__ __forceinline__ int wg_of_unit(const SkParams& p, long u) {
+  if (p.aligned) {
+    const long t = u / p.C;
+    return (int)(((t + 1) * p.P - 1) / p.T);
+  }
+  const long U = (long)p.T * p.C;
+  return (int)(((u + 1) * p.P - 1) / U);
+}
+
+template <int WF, int NMAT, int NCT, int SPS>
+struct Stage {
+  u32x4 w[NMAT][SPS][WF ? 1 : 2];
+  uint32_t e[NMAT];
+  u32x4 b[NCT][SPS][2];
+};
+
+// Position of a stage: unit index (== packed block index), superblock within the tile, part.
+struct Pos {
+  int st, unit, c, part;
+};
+
+template <int SPU>
+__device__ __forceinline__ void advance(Pos& q, int C) {
+  ++q.st;
+  if (++q.part == SPU) {
+    q.part = 0;
+    ++q.unit;
+    if (++q.c == C) q.c = 0;
+  }
+}
+
+template <int WF, int NMAT, int NCT, int SPS>
+__device__ __forceinline__ void load_stage(Stage<WF, NMAT, NCT, SPS>& s, const SkParams& p, const Pos& q,
+                                           int lane) {
+  constexpr int BLK = WF ? kBfp8Block : kBf16Block;
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat) {
+    const uint8_t* blk = (mat ? p.w1 : p.w0) + (size_t)q.unit * BLK;
+#pragma unroll
+    for (int jj = 0; jj < SPS; ++jj) {
+      const int j = q.part * SPS + jj;
+      if constexpr (WF) {
+        s.w[mat][jj][0] = ld_stream((const u32x4*)(blk + j * 1024 + lane * 16));
+      } else {
+        s.w[mat][jj][0] = ld_stream((const u32x4*)(blk + j * 2048 + lane * 16));
+        s.w[mat][jj][1] = ld_stream((const u32x4*)(blk + j * 2048 + 1024 + lane * 16));
+      }
+    }
+    if constexpr (WF) s.e[mat] = ld_stream((const uint32_t*)(blk + 4096 + lane * 4));
+  }
+  const int quarter = lane >> 4;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int m = ct * 16 + (lane & 15);
+#pragma unroll
+    for (int jj = 0; jj < SPS; ++jj) {
+      const int j = q.part * SPS + jj;
+      if (m < p.M) {
+        const uint16_t* bp = p.B + (size_t)m * p.K + q.c * kSuperK + j * 64 + quarter * 16;
+        s.b[ct][jj][0] = *(const u32x4*)bp;
+        s.b[ct][jj][1] = *(const u32x4*)(bp + 8);
+      } else {
+        s.b[ct][jj][0] = u32x4{0u, 0u, 0u, 0u};
+        s.b[ct][jj][1] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+}
+
+template <int WF, int NMAT, int NCT, int SPS>
+__device__ __forceinline__ void compute_stage(const Stage<WF, NMAT, NCT, SPS>& s, int part,
+                                              f32x4 (&acc)[NMAT][NCT][2]) {
+#pragma unroll
+  for (int jj = 0; jj < SPS; ++jj) {
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) {
+      if constexpr (WF) {
+        f16x8 a0, a1;
+        dq16(s.w[mat][jj][0], scale_pair(s.e[mat], part * SPS + jj), a0, a1);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+          acc[mat][ct][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              a0, __builtin_bit_cast(f16x8, s.b[ct][jj][0]), acc[mat][ct][0], 0, 0, 0);
+          acc[mat][ct][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+              a1, __builtin_bit_cast(f16x8, s.b[ct][jj][1]), acc[mat][ct][1], 0, 0, 0);
+        }
+      } else {
+        const bf16x8 a0 = __builtin_bit_cast(bf16x8, s.w[mat][jj][0]);
+        const bf16x8 a1 = __builtin_bit_cast(bf16x8, s.w[mat][jj][1]);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+          acc[mat][ct][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              a0, __builtin_bit_cast(bf16x8, s.b[ct][jj][0]), acc[mat][ct][0], 0, 0, 0);
+          acc[mat][ct][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              a1, __builtin_bit_cast(bf16x8, s.b[ct][jj][1]), acc[mat][ct][1], 0, 0, 0);
+        }
+      }
+    }
+  }
+}
+
+// Epilogue for one 16-row tile.  Lane l holds rows 4*(l/16) + v (v = 0..3) of token column l%16
+// (+16 per column tile) -- the 16x16 matrix-core output layout.
+template <int WF, int NMAT, int NCT>
+__device__ __forceinline__ void epilogue(const SkParams& p, int t, const f32x4 (&sum)[NMAT][NCT], int lane) {
+  const int nb = t * kTileRows + (lane >> 4) * 4;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int m = ct * 16 + (lane & 15);
+    if (m >= p.M) continue;
+    uint16_t o[4];
+    if constexpr (NMAT == 2) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float g = sum[0][ct][v], u = sum[1][ct][v];
+        if constexpr (WF) {
+          g = __builtin_amdgcn_ldexpf(g, p.rowexp0[nb + v] - p.bscale[m]);
+          u = __builtin_amdgcn_ldexpf(u, p.rowexp1[nb + v] - p.bscale[m]);
+        }
+        const float hv = g / (1.0f + expf(-g)) * u;
+        const uint16_t hb = f32_to_bf16(hv);
+        o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(bf16_to_f32(hb), p.hscale[m])) : hb;
+      }
+    } else {
+      float y[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        y[v] = sum[0][ct][v];
+        if constexpr (WF) y[v] = __builtin_amdgcn_ldexpf(y[v], p.rowexp0[nb + v] - p.bscale[m]);
+      }
+      if (p.residual) {
+        if (p.res_f32) {
+          const f32x4 r = *(const f32x4*)((const float*)p.residual + (size_t)m * p.N + nb);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) y[v] += r[v];
+        } else {
+          const u32x2 r = *(const u32x2*)((const uint16_t*)p.residual + (size_t)m * p.N + nb);
+          y[0] += bf16_to_f32((uint16_t)(r.x & 0xffffu));
+          y[1] += bf16_to_f32((uint16_t)(r.x >> 16));
+          y[2] += bf16_to_f32((uint16_t)(r.y & 0xffffu));
+          y[3] += bf16_to_f32((uint16_t)(r.y >> 16));
+        }
+      }
+      if (p.out_f32) {
+        *(f32x4*)((float*)p.out + (size_t)m * p.N + nb) = f32x4{y[0], y[1], y[2], y[3]};
+        continue;
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(y[v]);
+    }
+    *(u32x2*)((uint16_t*)p.out + (size_t)m * p.N + nb) =
+        u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+  }
+}
+
+// Tile cut by a workgroup boundary: publish this workgroup's partial, the last arrival sums all
+// partials in workgroup order and runs the epilogue.
+template <int WF, int NMAT, int NCT>
+__device__ void fixup(const SkParams& p, int w, int t, int t0, const f32x4 (&sum)[NMAT][NCT], int lane) {
+  constexpr int SLOT = NMAT * NCT * 64;
+  const int fw = wg_of_unit(p, (long)t * p.C);
+  const int lw = wg_of_unit(p, (long)t * p.C + p.C - 1);
+  f32x4* mine = (f32x4*)p.partials + (size_t)(2 * w + (t == t0 ? 0 : 1)) * SLOT;
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) mine[(mat * NCT + ct) * 64 + lane] = sum[mat][ct];
+  __threadfence();
+  int old = 0;
+  if (lane == 0) old = atomicAdd(p.counters + t, 1);
+  old = __shfl(old, 0);
+  if (old != lw - fw) return;
+  __threadfence();
+  f32x4 tot[NMAT][NCT];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) tot[mat][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int v = fw; v <= lw; ++v) {
+    if (v == w) {
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) tot[mat][ct] += sum[mat][ct];
+    } else {
+      int va, vb;
+      wg_range(p, v, va, vb);
+      const float* vs = p.partials + (size_t)(2 * v + (t == va / p.C ? 0 : 1)) * SLOT * 4;
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+          const float* e = vs + ((mat * NCT + ct) * 64 + lane) * 4;
+          tot[mat][ct] += f32x4{__hip_atomic_load(e + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                __hip_atomic_load(e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                __hip_atomic_load(e + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                __hip_atomic_load(e + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)};
+        }
+    }
+  }
+  epilogue<WF, NMAT, NCT>(p, t, tot, lane);
+  if (lane == 0) atomicExch(p.counters + t, 0);
+}
+
+template <int WF, int NMAT, int NCT, int NW>
+__global__ __launch_bounds__(NW * 64) void skinny_kernel(SkParams p) {
+  constexpr int SPS = (WF && NCT == 1) ? 4 : 2;  // K-steps per pipeline stage
+  constexpr int SPU = kSteps / SPS;              // stages per 256-K unit
+  constexpr int SLOT = NMAT * NCT * 64;          // f32x4 per parked partial
+  extern __shared__ f32x4 lds[];                 // [NW][kMaxSeg][SLOT]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = xcd_logical(blockIdx.x, p.P);
+  int a, b;
+  wg_range(p, w, a, b);
+  const int spt = SPU * p.C;  // stages per tile
+  const int sa = a * SPU + (int)((long)wave * (b - a) * SPU / NW);
+  const int sb = a * SPU + (int)((long)(wave + 1) * (b - a) * SPU / NW);
+
+  if (sa < sb) {
+    f32x4 acc[NMAT][NCT][2];
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) acc[mat][ct][0] = acc[mat][ct][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int tile0 = sa / spt;
+    int seg = 0, boundary = (tile0 + 1) * spt;
+    auto park = [&]() {
+      f32x4* slot = lds + (size_t)(wave * kMaxSeg + seg) * SLOT;
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+          slot[(mat * NCT + ct) * 64 + lane] = acc[mat][ct][0] + acc[mat][ct][1];
+          acc[mat][ct][0] = acc[mat][ct][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    Pos ld;
+    ld.st = sa;
+    ld.unit = sa / SPU;
+    ld.part = sa % SPU;
+    ld.c = ld.unit % p.C;
+    Stage<WF, NMAT, NCT, SPS> s0, s1;
+    load_stage(s0, p, ld, lane);
+    int part0 = ld.part;
+    for (int st = sa; st < sb; st += 2) {
+      advance<SPU>(ld, p.C);
+      int part1 = ld.part;
+      if (st + 1 < sb) load_stage(s1, p, ld, lane);
+      if (st >= boundary) {
+        park();
+        ++seg;
+        boundary += spt;
+      }
+      compute_stage(s0, part0, acc);
+      if (st + 1 >= sb) break;
+      advance<SPU>(ld, p.C);
+      part0 = ld.part;
+      if (st + 2 < sb) load_stage(s0, p, ld, lane);
+      if (st + 1 >= boundary) {
+        park();
+        ++seg;
+        boundary += spt;
+      }
+      compute_stage(s1, part1, acc);
+    }
+    park();
+  }
+  __syncthreads();
+  if (a >= b) return;
+  const int t0 = a / p.C, t1 = (b - 1) / p.C;
+  for (int t = t0 + wave; t <= t1; t += NW) {
+    f32x4 sum[NMAT][NCT];
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) sum[mat][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int v = 0; v < NW; ++v) {
+      const int va = a * SPU + (int)((long)v * (b - a) * SPU / NW);
+      const int vb = a * SPU + (int)((long)(v + 1) * (b - a) * SPU / NW);
+      if (va >= vb) continue;
+      const int vt0 = va / spt, vt1 = (vb - 1) / spt;
+      if (t < vt0 || t > vt1) continue;
+      const f32x4* slot = lds + (size_t)(v * kMaxSeg + (t - vt0)) * SLOT;
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) sum[mat][ct] += slot[(mat * NCT + ct) * 64 + lane];
+    }
+    if ((long)t * p.C >= a && (long)(t + 1) * p.C <= b)
+      epilogue<WF, NMAT, NCT>(p, t, sum, lane);
+    else
+      fixup<WF, NMAT, NCT>(p, w, t, t0, sum, lane);
+  }
+}
+
+// ---------------------------------------------------------------- bfp8 activation prep
+
+__global__ __launch_bounds__(256) void prep_kernel(const uint16_t* __restrict__ x, int H,
+                                                   const Trailer* tg, const Trailer* tu,
+                                                   uint16_t* __restrict__ x16, int* __restrict__ tx,
+                                                   int* __restrict__ th) {
+  __shared__ float smax[256];
+  __shared__ double ssum[256];
+  __shared__ int sexp;
+  const int m = blockIdx.x;
+  const uint16_t* xr = x + (size_t)m * H;
+  float mx = 0.f;
+  double ss = 0.0;
+  for (int k = threadIdx.x; k < H; k += 256) {
+    const float v = bf16_to_f32(xr[k]);
+    mx = fmaxf(mx, fabsf(v));
+    ss += (double)v * (double)v;
+  }
+  smax[threadIdx.x] = mx;
+  ssum[threadIdx.x] = ss;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      smax[threadIdx.x] = fmaxf(smax[threadIdx.x], smax[threadIdx.x + s]);
+      ssum[threadIdx.x] += ssum[threadIdx.x + s];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    int e = 0;
+    const float mxa = smax[0];
+    if (mxa > 0.f) frexpf(mxa, &e);
+    const int txm = mxa > 0.f ? 15 - e : 0;
+    const double gn = __longlong_as_double((long long)tg->max_row_norm_bits);
+    const double un = __longlong_as_double((long long)tu->max_row_norm_bits);
+    const double bound = ssum[0] * gn * un * (1.0 + 1.0 / 64.0);
+    int eb = 0;
+    if (bound > 0.0) frexp(bound, &eb);
+    tx[m] = txm;
+    th[m] = bound > 0.0 ? 15 - eb : 0;
+    sexp = txm;
+  }
+  __syncthreads();
+  const int txm = sexp;
+  uint16_t* orow = x16 + (size_t)m * H;
+  for (int k = threadIdx.x; k < H; k += 256)
+    orow[k] = f32_to_f16_bits(__builtin_amdgcn_ldexpf(bf16_to_f32(xr[k]), txm));
+}
+
+// ---------------------------------------------------------------- host side
+
+int plan_skinny(int rows, int K, int M, int num_cus, SkinnyPlan* plan) {
+  (void)M;
+  if (rows <= 0 || K <= 0 || rows % kTileRows || K % kSuperK) return -1;
+  const int NW = 8;
+  const int T = rows / kTileRows, C = K / kSuperK;
+  const long U = (long)T * C;
+  int P = num_cus < 1 ? 1 : num_cus;
+  if (P > kMaxWorkgroups) P = kMaxWorkgroups;
+  if (P > T) P = T;
+  // A wave must touch at most kMaxSeg (= 2) tiles: its range (<= ceil(ceil(U/P)*SPU/NW) stages,
+  // SPU <= 2) must not exceed one tile's stages plus one.
+  for (;;) {
+    const long R = (U + P - 1) / P;
+    const long L = (R * 2 + NW - 1) / NW;
+    if (L <= 2L * C + 1 || P >= T) break;
+    ++P;
+  }
+  const char* env = getenv("QMLP_ALIGNED");
+  plan->P = P;
+  plan->NW = NW;
+  plan->T = T;
+  plan->C = C;
+  plan->aligned = (env && env[0] == '1') ? 1 : 0;
+  return 0;
+}
+
+template <int WF, int NMAT, int NCT>
+static int launch_proj(const SkParams& p, hipStream_t s) {
+  constexpr int NW = 8;
+  const size_t lds = (size_t)NW * kMaxSeg * NMAT * NCT * 64 * sizeof(f32x4);
+  hipLaunchKernelGGL((skinny_kernel<WF, NMAT, NCT, NW>), dim3(p.P), dim3(NW * 64), lds, s, p);
+  return check_launch("skinny_kernel");
+}
+
+template <int WF, int NMAT>
+static int launch_proj_m(const SkParams& p, hipStream_t s) {
+  return p.M <= 16 ? launch_proj<WF, NMAT, 1>(p, s) : launch_proj<WF, NMAT, 2>(p, s);
+}
+
+int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s) {
+  const WsLayout L = ws_layout(a.M, a.H, a.I, a.fmt);
+  const int fmt = a.fmt;
+  int* tx = (int*)(a.ws + L.tx);
+  int* th = (int*)(a.ws + L.th);
+  uint16_t* x16 = (uint16_t*)(a.ws + L.x16);
+  uint16_t* h = (uint16_t*)(a.ws + L.h);
+  if (fmt == 1) {
+    const Trailer* tg = (const Trailer*)(a.wg + trailer_offset(a.I, a.H, 1));
+    const Trailer* tu = (const Trailer*)(a.wu + trailer_offset(a.I, a.H, 1));
+    hipLaunchKernelGGL(prep_kernel, dim3(a.M), dim3(256), 0, s, (const uint16_t*)a.x, a.H, tg, tu, x16, tx, th);
+    int rc = check_launch("prep_kernel");
+    if (rc) return rc;
+  }
+  SkinnyPlan pg, pd;
+  if (plan_skinny(a.I, a.H, 32, num_cus, &pg) || plan_skinny(a.H, a.I, 32, num_cus, &pd))
+    return set_error(-1, "bad projection shape H=%d I=%d", a.H, a.I);
+  // M > 32 runs in 32-token chunks through the same kernels (the tiled path handles large M).
+  for (int m0 = 0; m0 < a.M; m0 += 32) {
+    const int mc = a.M - m0 < 32 ? a.M - m0 : 32;
+    SkParams g{};
+    g.w0 = a.wg;
+    g.w1 = a.wu;
+    g.rowexp0 = (const int*)(a.wg + rowexp_offset(a.I, a.H, fmt));
+    g.rowexp1 = (const int*)(a.wu + rowexp_offset(a.I, a.H, fmt));
+    g.B = fmt == 1 ? x16 + (size_t)m0 * a.H : (const uint16_t*)a.x + (size_t)m0 * a.H;
+    g.M = mc;
+    g.K = a.H;
+    g.N = a.I;
+    g.C = pg.C;
+    g.T = pg.T;
+    g.P = pg.P;
+    g.aligned = pg.aligned;
+    g.bscale = tx + m0;
+    g.hscale = th + m0;
+    g.out = h + (size_t)m0 * a.I;
+    g.residual = nullptr;
+    g.out_f32 = 0;
+    g.res_f32 = 0;
+    g.partials = (float*)(a.ws + L.part_gu);
+    g.counters = (int*)(a.ws + L.counters_gu);
+    int rc = fmt == 1 ? launch_proj_m<1, 2>(g, s) : launch_proj_m<0, 2>(g, s);
+    if (rc) return rc;
+    SkParams d{};
+    d.w0 = a.wd;
+    d.w1 = nullptr;
+    d.rowexp0 = (const int*)(a.wd + rowexp_offset(a.H, a.I, fmt));
+    d.rowexp1 = nullptr;
+    d.B = h + (size_t)m0 * a.I;
+    d.M = mc;
+    d.K = a.I;
+    d.N = a.H;
+    d.C = pd.C;
+    d.T = pd.T;
+    d.P = pd.P;
+    d.aligned = pd.aligned;
+    d.bscale = th + m0;
+    d.hscale = nullptr;
+    d.out = (uint8_t*)a.out + (size_t)m0 * a.H * (a.out_f32 ? 4 : 2);
+    d.residual = a.residual ? (const uint8_t*)a.residual + (size_t)m0 * a.H * (a.res_f32 ? 4 : 2) : nullptr;
+    d.out_f32 = a.out_f32;
+    d.res_f32 = a.res_f32;
+    d.partials = (float*)(a.ws + L.part_d);
+    d.counters = (int*)(a.ws + L.counters_d);
+    rc = fmt == 1 ? launch_proj_m<1, 1>(d, s) : launch_proj_m<0, 1>(d, s);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+}  // namespace qmlp

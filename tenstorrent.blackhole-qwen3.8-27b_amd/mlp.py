@@ -1,0 +1,343 @@
+"""Qwen3 SwiGLU MLP for MI355X: the host-side mirror of the reference module.
+
+Reference interface being replaced (``docker/qwen-c2-graft/graft/mlp.py``):
+
+* ``MLPWeights`` (``mlp.py:15-20``): w1 = gate_proj, w2 = down_proj, w3 = up_proj.
+* ``load_mlp_weights(mesh_device, state_dict, tensor_cache_path=None, args=None)``
+  (``mlp.py:45-169``): converts the HF tensors ``{gate,up,down}_proj.weight`` into device tiles.
+* ``Qwen36MLP(mesh_device, state_dict, tensor_cache_path=None, args=None, tt_ccl=None)`` with
+  ``forward(x)`` (``mlp.py:359-423``): ``down(silu(gate(x)) * up(x))`` on a ``[1, 1, M, H]`` bf16
+  activation; the decoder layer then adds the residual (``layer.py:354-357``), which
+  ``forward(x, residual=h)`` fuses.
+
+Shapes: x ``[1, 1, M, H]`` or ``[M, H]`` (any leading dims multiply into M), bf16, on the GPU.
+Errors: ``ValueError`` for wrong shape/dtype/device (as ``FusedProjection.__call__``,
+``scripts/ci/fused_1d.py:124-128``), ``QmlpError`` for launch failures.  There is no CPU fallback.
+"""
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+WEIGHT_FORMATS = ("bf16", "bfp8")
+
+
+@dataclass
+class PackedWeight:
+    """One weight matrix in the library's packed layout (device bytes + shape + format)."""
+
+    buf: torch.Tensor  # uint8 device tensor, qmlp_packed_bytes(rows, cols, fmt) bytes
+    rows: int
+    cols: int
+    fmt: str
+    max_row_norm: float = 0.0
+    flushed_groups: int = 0
+
+    @property
+    def fmt_code(self):
+        return _lib.FORMATS[self.fmt]
+
+    @property
+    def nbytes(self):
+        return self.buf.numel()
+
+    @property
+    def stream_bytes(self):
+        """Bytes of the weight values the forward pass streams (excludes row exponents/trailer)."""
+        per_value = 17 / 16 if self.fmt == "bfp8" else 2
+        return int(self.rows * self.cols * per_value)
+
+    def data_ptr(self):
+        return self.buf.data_ptr()
+
+
+def _check_device_tensor(t, name, dtype=None):
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on the GPU, got {t.device}")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def quantize_bfp8(w, stream=None):
+    """Canonical bfp8 of a bf16 ``[rows, cols]`` GPU tensor -> ``(q int8 [rows, cols], e8 uint8 [rows, cols/16])``."""
+    _check_device_tensor(w, "w", torch.bfloat16)
+    if w.dim() != 2:
+        raise ValueError("w must be 2-D")
+    rows, cols = w.shape
+    q = torch.empty((rows, cols), dtype=torch.int8, device=w.device)
+    e8 = torch.empty((rows, cols // 16), dtype=torch.uint8, device=w.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=w.device)
+    _lib.check(_lib.lib().qmlp_quantize_bfp8(_lib.ptr(w), rows, cols, _lib.ptr(q), _lib.ptr(e8), _lib.ptr(bad),
+                                             _lib.stream_handle(stream)), "qmlp_quantize_bfp8")
+    if int(bad.item()):
+        raise ValueError(f"weight holds non-finite values in {int(bad.item())} groups")
+    return q, e8
+
+
+def _read_info(pw, stream=None):
+    norm = ctypes.c_double(0.0)
+    flushed = ctypes.c_uint32(0)
+    _lib.check(_lib.lib().qmlp_packed_info(_lib.ptr(pw.buf), pw.rows, pw.cols, pw.fmt_code, ctypes.byref(norm),
+                                           ctypes.byref(flushed), _lib.stream_handle(stream)), "qmlp_packed_info")
+    pw.max_row_norm = float(norm.value)
+    pw.flushed_groups = int(flushed.value)
+    return pw
+
+
+def pack_canonical_bfp8(q, e8, strict=True, stream=None):
+    """Pack canonical bfp8 (q int8 [rows, cols], e8 uint8 [rows, cols/16]) into the device layout."""
+    _check_device_tensor(q, "q", torch.int8)
+    _check_device_tensor(e8, "e8", torch.uint8)
+    rows, cols = q.shape
+    if tuple(e8.shape) != (rows, cols // 16):
+        raise ValueError("e8 must be [rows, cols/16]")
+    nbytes = _lib.lib().qmlp_packed_bytes(rows, cols, _lib.FMT_BFP8)
+    if nbytes == 0:
+        raise ValueError(f"unsupported shape {rows}x{cols}: rows must be a multiple of 16 and cols of 256")
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    _lib.check(_lib.lib().qmlp_pack(_lib.ptr(q), _lib.ptr(e8), rows, cols, _lib.FMT_BFP8, _lib.ptr(buf), nbytes,
+                                    _lib.stream_handle(stream)), "qmlp_pack")
+    pw = _read_info(PackedWeight(buf, rows, cols, "bfp8"), stream)
+    if strict and pw.flushed_groups:
+        raise ValueError(f"{pw.flushed_groups} bfp8 groups lie more than 19 binades below their row maximum")
+    return pw
+
+
+def pack_weight(w, fmt="bfp8", strict=True, stream=None):
+    """bf16 ``[rows, cols]`` GPU tensor (HF layout: [out, in]) -> PackedWeight in ``fmt``."""
+    if fmt not in WEIGHT_FORMATS:
+        raise ValueError(f"weight format must be one of {WEIGHT_FORMATS}, got {fmt!r}")
+    _check_device_tensor(w, "w", torch.bfloat16)
+    if w.dim() != 2:
+        raise ValueError("w must be 2-D")
+    if fmt == "bfp8":
+        q, e8 = quantize_bfp8(w, stream)
+        return pack_canonical_bfp8(q, e8, strict=strict, stream=stream)
+    rows, cols = w.shape
+    nbytes = _lib.lib().qmlp_packed_bytes(rows, cols, _lib.FMT_BF16)
+    if nbytes == 0:
+        raise ValueError(f"unsupported shape {rows}x{cols}: rows must be a multiple of 16 and cols of 256")
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+    _lib.check(_lib.lib().qmlp_pack(_lib.ptr(w), None, rows, cols, _lib.FMT_BF16, _lib.ptr(buf), nbytes,
+                                    _lib.stream_handle(stream)), "qmlp_pack")
+    return _read_info(PackedWeight(buf, rows, cols, "bf16"), stream)
+
+
+def unpack_bfp8(pw, stream=None):
+    """Packed bfp8 -> canonical (q, e8) (lossless for unflushed groups)."""
+    if pw.fmt != "bfp8":
+        raise ValueError("unpack_bfp8 needs a bfp8 weight")
+    q = torch.empty((pw.rows, pw.cols), dtype=torch.int8, device=pw.buf.device)
+    e8 = torch.empty((pw.rows, pw.cols // 16), dtype=torch.uint8, device=pw.buf.device)
+    _lib.check(_lib.lib().qmlp_unpack_bfp8(_lib.ptr(pw.buf), pw.rows, pw.cols, _lib.ptr(q), _lib.ptr(e8),
+                                           _lib.stream_handle(stream)), "qmlp_unpack_bfp8")
+    return q, e8
+
+
+def dequantize(pw, stream=None):
+    """Packed weight -> float32 ``[rows, cols]`` via the kernels' own dequant routine."""
+    out = torch.empty((pw.rows, pw.cols), dtype=torch.float32, device=pw.buf.device)
+    _lib.check(_lib.lib().qmlp_dequant_packed(_lib.ptr(pw.buf), pw.rows, pw.cols, pw.fmt_code, _lib.ptr(out),
+                                              _lib.stream_handle(stream)), "qmlp_dequant_packed")
+    return out
+
+
+def workspace_bytes(M, H, I, fmt):
+    n = _lib.lib().qmlp_workspace_bytes(M, H, I, _lib.FORMATS[fmt])
+    if n == 0:
+        raise ValueError(f"unsupported sizes M={M} H={H} I={I} fmt={fmt}")
+    return n
+
+
+def new_workspace(M, H, I, fmt, device, stream=None):
+    """Allocate and initialise a forward workspace (outside any graph capture)."""
+    n = workspace_bytes(M, H, I, fmt)
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    _lib.check(_lib.lib().qmlp_workspace_init(_lib.ptr(ws), n, _lib.stream_handle(stream)), "qmlp_workspace_init")
+    return ws
+
+
+@dataclass(frozen=True)
+class MLPWeights:
+    """Packed MLP weights; field names follow ``docker/qwen-c2-graft/graft/mlp.py:15-20``."""
+
+    w1: PackedWeight  # gate_proj [I, H]
+    w2: PackedWeight  # down_proj [H, I]
+    w3: PackedWeight  # up_proj   [I, H]
+
+    @property
+    def hidden(self):
+        return self.w1.cols
+
+    @property
+    def intermediate(self):
+        return self.w1.rows
+
+    @property
+    def fmt(self):
+        return self.w1.fmt
+
+    @property
+    def stream_bytes(self):
+        return self.w1.stream_bytes + self.w2.stream_bytes + self.w3.stream_bytes
+
+
+def load_mlp_weights(device, state_dict, tensor_cache_path=None, args=None, weight_format="bfp8"):
+    """Per-layer MLP state -> MLPWeights (``mlp.py:45-169``).
+
+    ``state_dict`` holds ``gate_proj.weight`` / ``up_proj.weight`` ``[I, H]`` and
+    ``down_proj.weight`` ``[H, I]`` (HF layout).  ``tensor_cache_path`` (a directory) enables the
+    on-disk cache of packed weights, like the reference's ``cache_file_name``.  ``weight_format``
+    may also come from ``args.mlp_weight_format``.
+    """
+    fmt = getattr(args, "mlp_weight_format", weight_format) if args is not None else weight_format
+    if fmt not in WEIGHT_FORMATS:
+        raise ValueError(f"weight format must be one of {WEIGHT_FORMATS}, got {fmt!r}")
+    device = torch.device(device) if not isinstance(device, torch.device) else device
+    if device.type != "cuda":
+        raise ValueError(f"device must be a GPU, got {device}")
+    names = {"w1": "gate_proj", "w2": "down_proj", "w3": "up_proj"}
+    packed = {}
+    for field, name in names.items():
+        cache = None
+        if tensor_cache_path is not None:
+            from . import weight_cache
+
+            cache = weight_cache.cache_file(tensor_cache_path, name, fmt)
+            pw = weight_cache.load(cache, device) if os.path.exists(cache) else None
+            if pw is not None:
+                packed[field] = pw
+                continue
+        w = state_dict[f"{name}.weight"]
+        if not isinstance(w, torch.Tensor):
+            w = torch.as_tensor(w)
+        w = w.to(device=device, dtype=torch.bfloat16).contiguous()
+        packed[field] = pack_weight(w, fmt)
+        del w
+        if cache is not None:
+            from . import weight_cache
+
+            weight_cache.save(cache, packed[field])
+    weights = MLPWeights(**packed)
+    I, H = weights.w1.rows, weights.w1.cols
+    if (weights.w3.rows, weights.w3.cols) != (I, H) or (weights.w2.rows, weights.w2.cols) != (H, I):
+        raise ValueError("gate/up must be [I, H] and down [H, I]")
+    if len({weights.w1.fmt, weights.w2.fmt, weights.w3.fmt}) != 1:
+        raise ValueError("all three weights must share one format")
+    return weights
+
+
+def mlp_forward(x2d, weights, residual=None, out=None, workspace=None, stream=None, out_dtype=None):
+    """``out = residual + down(silu(gate(x)) * up(x))`` for a 2-D bf16 ``[M, H]`` GPU tensor.
+
+    ``residual`` may be bf16 or fp32; ``out`` (or ``out_dtype`` when ``out`` is None) may be bf16
+    (rounded once to nearest-even) or fp32 (the unrounded fp32 sum).  ``out`` may be the residual
+    tensor itself (in-place residual update).
+    """
+    _check_device_tensor(x2d, "x", torch.bfloat16)
+    M, H = x2d.shape
+    I = weights.intermediate
+    if H != weights.hidden:
+        raise ValueError(f"x has hidden size {H}, weights expect {weights.hidden}")
+    flags = 0
+    if residual is not None:
+        _check_device_tensor(residual, "residual")
+        if residual.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("residual must be bf16 or fp32")
+        if tuple(residual.shape) != (M, H):
+            raise ValueError("residual must match x")
+        if residual.dtype == torch.float32:
+            flags |= _lib.RESIDUAL_F32
+    if out is None:
+        dt = torch.bfloat16 if out_dtype is None else out_dtype
+        if dt not in (torch.bfloat16, torch.float32):
+            raise ValueError("out_dtype must be bf16 or fp32")
+        out = torch.empty((M, H), dtype=dt, device=x2d.device)
+    else:
+        _check_device_tensor(out, "out")
+        if out.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("out must be bf16 or fp32")
+        if tuple(out.shape) != (M, H):
+            raise ValueError("out must match x")
+    if out.dtype == torch.float32:
+        flags |= _lib.OUT_F32
+    if workspace is None:
+        workspace = new_workspace(M, H, I, weights.fmt, x2d.device, stream)
+    rc = _lib.lib().qmlp_forward_ex(_lib.ptr(x2d), _lib.ptr(weights.w1.buf), _lib.ptr(weights.w3.buf),
+                                    _lib.ptr(weights.w2.buf), _lib.ptr(residual), _lib.ptr(out),
+                                    _lib.ptr(workspace), workspace.numel(), M, H, I, weights.w1.fmt_code, flags,
+                                    _lib.stream_handle(stream))
+    _lib.check(rc, "qmlp_forward")
+    return out
+
+
+class Qwen36MLP:
+    """SwiGLU feed-forward network (``docker/qwen-c2-graft/graft/mlp.py:359-423``) on MI355X.
+
+    ``Qwen36MLP(device, state_dict, tensor_cache_path=None, args=None, tt_ccl=None,
+    weight_format="bfp8", max_tokens=2048)``; ``forward(x, residual=None, out=None)``.
+    The workspace for up to ``max_tokens`` rows is allocated here, so ``forward`` allocates
+    nothing but its output (and nothing at all when ``out`` is given): it may run inside a HIP
+    graph capture.
+    """
+
+    def __init__(self, mesh_device, state_dict, tensor_cache_path=None, args=None, tt_ccl=None,
+                 weight_format="bfp8", max_tokens=2048):
+        self.device = torch.device(mesh_device) if not isinstance(mesh_device, torch.device) else mesh_device
+        self.args = args
+        self.tt_ccl = tt_ccl
+        self.weights = load_mlp_weights(self.device, state_dict, tensor_cache_path, args, weight_format)
+        self.max_tokens = int(max_tokens)
+        self._workspace = new_workspace(self.max_tokens, self.weights.hidden, self.weights.intermediate,
+                                        self.weights.fmt, self.device)
+
+    @property
+    def weight_format(self):
+        return self.weights.fmt
+
+    def _workspace_for(self, M):
+        if M > self.max_tokens:
+            # Outside graph capture only: grow once.
+            if torch.cuda.is_current_stream_capturing():
+                raise ValueError(f"M={M} exceeds max_tokens={self.max_tokens} during graph capture")
+            self.max_tokens = M
+            self._workspace = new_workspace(M, self.weights.hidden, self.weights.intermediate, self.weights.fmt,
+                                            self.device)
+        return self._workspace
+
+    def forward(self, x, residual=None, out=None, out_dtype=None):
+        if not isinstance(x, torch.Tensor) or x.dtype != torch.bfloat16:
+            raise ValueError("BF16 activation tensor required")
+        if x.dim() < 1 or x.shape[-1] != self.weights.hidden:
+            raise ValueError(f"activation must end in hidden size {self.weights.hidden}, got {tuple(x.shape)}")
+        if x.device.type != "cuda":
+            raise ValueError("activation must be on the GPU")
+        shape = x.shape
+        x2d = x.reshape(-1, shape[-1])
+        if not x2d.is_contiguous():
+            x2d = x2d.contiguous()
+        M = x2d.shape[0]
+        if M == 0:
+            raise ValueError("empty activation")
+        r2d = None
+        if residual is not None:
+            if tuple(residual.shape) != tuple(shape):
+                raise ValueError("residual must have the activation's shape")
+            r2d = residual.reshape(M, shape[-1])
+        o2d = None
+        if out is not None:
+            if tuple(out.shape) != tuple(shape):
+                raise ValueError("out must have the activation's shape")
+            o2d = out.reshape(M, shape[-1])
+        y = mlp_forward(x2d, self.weights, residual=r2d, out=o2d, workspace=self._workspace_for(M),
+                        out_dtype=out_dtype)
+        return y.reshape(shape) if out is None else out
+
+    __call__ = forward

@@ -1,0 +1,78 @@
+"""Seeded synthetic MLP workloads (activations and random-init weights of the Qwen3 shapes).
+
+There are no checkpoints offline, so weights are ``N(0, 0.02)`` bf16 and activations ``N(0, 1)``
+bf16, optionally scaled per hidden channel by an RMSNorm-like gain ``U(0.5, 1.5)``.  The seeds follow
+the reference's convention of separate activation and weight seeds (``1000 + seed`` /
+``2000 + seed``, ``optimisation/ttnn-op/c1e_gateup/c1e_gateup_card_b.py:128-151``).
+"""
+from dataclasses import dataclass
+
+import torch
+
+QWEN3_27B = {"hidden": 5120, "intermediate": 17408}
+PLUMBING = {"hidden": 1024, "intermediate": 3072}
+X_SEED = 1000
+W_SEED = 2000
+
+
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    hidden: int
+    intermediate: int
+    tokens: int
+    fmt: str
+    gain: bool  # RMSNorm-like per-channel gain on the activations
+
+    def weight_bytes(self):
+        per = 17 / 16 if self.fmt == "bfp8" else 2
+        return int(3 * self.hidden * self.intermediate * per)
+
+    def algorithmic_bytes(self):
+        """Weights streamed once + activation read + output write + residual read (bf16):
+        W + 4*M*H bytes per layer."""
+        return self.weight_bytes() + 4 * self.tokens * self.hidden
+
+    def flops(self):
+        return 6 * self.tokens * self.hidden * self.intermediate
+
+
+WORKLOADS = {
+    "plumbing-h1024-i3072-m1-bf16": Workload("plumbing-h1024-i3072-m1-bf16", 1024, 3072, 1, "bf16", False),
+    "qwen3-27b-mlp-m16-bf16": Workload("qwen3-27b-mlp-m16-bf16", 5120, 17408, 16, "bf16", True),
+    "qwen3-27b-mlp-m16-bfp8": Workload("qwen3-27b-mlp-m16-bfp8", 5120, 17408, 16, "bfp8", True),
+    "qwen3-27b-mlp-m1-bfp8": Workload("qwen3-27b-mlp-m1-bfp8", 5120, 17408, 1, "bfp8", True),
+    "qwen3-27b-mlp-m32-bfp8": Workload("qwen3-27b-mlp-m32-bfp8", 5120, 17408, 32, "bfp8", True),
+    "qwen3-27b-mlp-prefill-m2048-bfp8": Workload("qwen3-27b-mlp-prefill-m2048-bfp8", 5120, 17408, 2048, "bfp8", False),
+}
+
+
+def _gen(seed, device):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def activations(tokens, hidden, seed=X_SEED, gain=True, device="cuda"):
+    """bf16 ``[tokens, hidden]``: N(0,1), times a per-channel gain U(0.5, 1.5) when ``gain``."""
+    g = _gen(seed, device)
+    x = torch.randn((tokens, hidden), generator=g, device=device, dtype=torch.float32)
+    if gain:
+        x = x * (0.5 + torch.rand((hidden,), generator=g, device=device, dtype=torch.float32))
+    return x.to(torch.bfloat16)
+
+
+def weight(rows, cols, seed, std=0.02, device="cuda"):
+    """bf16 ``[rows, cols]`` ~ N(0, std)."""
+    g = _gen(seed, device)
+    return (torch.randn((rows, cols), generator=g, device=device, dtype=torch.float32) * std).to(torch.bfloat16)
+
+
+def state_dict(hidden, intermediate, layer=0, device="cuda"):
+    """HF-layout MLP tensors of one layer, seeds 2000 + 3*layer + {0: gate, 1: up, 2: down}."""
+    base = W_SEED + 3 * layer
+    return {
+        "gate_proj.weight": weight(intermediate, hidden, base + 0, device=device),
+        "up_proj.weight": weight(intermediate, hidden, base + 1, device=device),
+        "down_proj.weight": weight(hidden, intermediate, base + 2, device=device),
+    }

@@ -1,0 +1,282 @@
+"""GPU parity: the HIP path through the C ABI against the CPU oracle on the same seeded inputs.
+
+Integer work (quantisation, packing, unpacking, dequantisation) must be bit-exact.  The MLP output
+must satisfy max|out - oracle| <= 1e-2 * RMS(oracle), the oracle being the fp32 SwiGLU on the
+identically dequantised weights (scripts/ci/mlp-sweep.py:121-126, layer.py:357)."""
+import numpy as np
+import pytest
+
+from oracle import bf16 as obf16
+from oracle import bfp8 as obfp8
+from oracle import mlp as omlp
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _bits(t):
+    import torch
+
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _host_weights(pkg, sd, fmt):
+    """fp32 host copies of the identically dequantised weights (keyed by HF name)."""
+    out = {}
+    for name in ("gate_proj", "up_proj", "down_proj"):
+        w = sd[f"{name}.weight"]
+        if fmt == "bfp8":
+            q, e8 = pkg.quantize_bfp8(w)
+            out[name] = obfp8.dequantize(q.cpu().numpy(), e8.cpu().numpy())
+        else:
+            out[name] = obf16.bits_to_f32(_bits(w))
+    return out
+
+
+def _oracle(xf, hw, residual=True):
+    return omlp.swiglu(xf, hw["gate_proj"], hw["up_proj"], hw["down_proj"], residual=xf if residual else None)
+
+
+def _check(y, ref, what):
+    """The stated bar on an fp32 (unrounded) output."""
+    ok, err, bound = omlp.tolerance_ok(y, ref, TOL)
+    print(f"{what}: max|err|={err:.4e} bound={bound:.4e} ({err / bound:.2f} of the bar)", flush=True)
+    assert ok, f"{what}: {err} > {bound}"
+    return err / bound
+
+
+def _check_bf16(y, ref, what):
+    """A bf16 output cannot be closer to the fp32 oracle than its own rounding: elementwise
+    |y - ref| <= 1e-2 * RMS(ref) + half a bf16 ulp of ref."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    rms = float(np.sqrt(np.mean(ref * ref)))
+    _, e = np.frexp(np.abs(ref))
+    half_ulp = np.ldexp(1.0, e - 9)  # |ref| in [2^(e-1), 2^e): bf16 ulp 2^(e-8)
+    excess = np.abs(y - ref) - half_ulp
+    worst = float(excess.max())
+    print(f"{what} (bf16 out): max(|err| - half ulp)={worst:.4e} bar={TOL * rms:.4e}", flush=True)
+    assert worst <= TOL * rms, f"{what}: {worst} > {TOL * rms}"
+
+
+# ---------------------------------------------------------------- load-time kernels (bit-exact)
+
+
+def test_quantize_bit_exact(pkg, cuda):
+    import torch
+    from qwen_mlp_amd import workloads
+
+    w = workloads.weight(512, 5120, seed=77, device=cuda)
+    edge = np.array([[0] * 16, [0x7F7F] + [1] * 15, [1, 0x8002] + [0] * 14, [0x3F80] * 15 + [0xBF81]], np.uint16)
+    edge_words = np.tile(edge.reshape(1, 64), (16, 4))  # 16 rows x 256 cols
+    scales = torch.tensor([1e-30, 1e-3, 1.0, 3e4], device=cuda).repeat_interleave(128).view(512, 1)
+    wide = (torch.randn((512, 5120), device=cuda, generator=torch.Generator(cuda).manual_seed(3)) * scales)
+    for mat in (w, wide.to(torch.bfloat16)):
+        q, e8 = pkg.quantize_bfp8(mat)
+        qo, eo = obfp8.quantize(_bits(mat))
+        assert np.array_equal(q.cpu().numpy(), qo)
+        assert np.array_equal(e8.cpu().numpy(), eo)
+    ew = torch.from_numpy(edge_words.view(np.int16)).to(cuda).view(torch.bfloat16).contiguous()
+    q, e8 = pkg.quantize_bfp8(ew)
+    qo, eo = obfp8.quantize(edge_words)
+    assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(e8.cpu().numpy(), eo)
+
+
+def test_quantize_rejects_non_finite(pkg, cuda):
+    import torch
+
+    w = torch.zeros((16, 256), dtype=torch.bfloat16, device=cuda)
+    w[3, 17] = float("inf")
+    with pytest.raises(ValueError):
+        pkg.quantize_bfp8(w)
+
+
+@pytest.mark.parametrize("rows,cols", [(48, 768), (3072, 1024), (1024, 3072)])
+def test_pack_matches_oracle_layout(pkg, cuda, rows, cols):
+    from qwen_mlp_amd import workloads
+
+    w = workloads.weight(rows, cols, seed=rows + cols, device=cuda)
+    wb = _bits(w)
+    # bfp8
+    q, e8 = pkg.quantize_bfp8(w)
+    pw = pkg.pack_canonical_bfp8(q, e8)
+    qo, eo = obfp8.quantize(wb)
+    tiles, rowexp, flushed = obfp8.pack_tiles(qo, eo)
+    buf = pw.buf.cpu().numpy()
+    assert np.array_equal(buf[: tiles.size], tiles)
+    assert np.array_equal(buf[tiles.size: tiles.size + rows * 4].view(np.int32), rowexp)
+    assert pw.flushed_groups == flushed == 0
+    norms = obfp8.row_norms(obfp8.dequantize(qo, eo))
+    assert abs(pw.max_row_norm - norms.max()) <= 1e-9 * norms.max()
+    qu, eu = pkg.unpack_bfp8(pw)
+    assert np.array_equal(qu.cpu().numpy(), qo) and np.array_equal(eu.cpu().numpy(), eo)
+    assert np.array_equal(pkg.dequantize(pw).cpu().numpy(), obfp8.dequantize(qo, eo))
+    # bf16
+    pb = pkg.pack_weight(w, "bf16")
+    tb = obfp8.pack_tiles_bf16(wb)
+    assert np.array_equal(pb.buf.cpu().numpy()[: tb.size], tb)
+    assert np.array_equal(pkg.dequantize(pb).cpu().numpy(), obf16.bits_to_f32(wb))
+
+
+def test_pack_reports_flushed_groups(pkg, cuda):
+    import torch
+
+    w = torch.zeros((16, 256), dtype=torch.float32, device=cuda)
+    w[:, :16] = 1.0
+    w[:, 16:32] = 2.0 ** -19
+    w[:, 32:48] = 2.0 ** -20
+    q, e8 = pkg.quantize_bfp8(w.to(torch.bfloat16))
+    with pytest.raises(ValueError):
+        pkg.pack_canonical_bfp8(q, e8)
+    pw = pkg.pack_canonical_bfp8(q, e8, strict=False)
+    assert pw.flushed_groups == 16
+    d = pkg.dequantize(pw).cpu().numpy()
+    assert (d[:, 16:32] == 2.0 ** -19).all() and (d[:, 32:48] == 0).all()
+
+
+# ---------------------------------------------------------------- forward parity
+
+
+@pytest.mark.parametrize("name", ["plumbing-h1024-i3072-m1-bf16", "qwen3-27b-mlp-m16-bf16", "qwen3-27b-mlp-m16-bfp8",
+                                  "qwen3-27b-mlp-m1-bfp8", "qwen3-27b-mlp-m32-bfp8"])
+def test_forward_workloads(pkg, cuda, name):
+    import torch
+    from qwen_mlp_amd import workloads
+
+    wl = workloads.WORKLOADS[name]
+    print(f"case {name}", flush=True)
+    sd = workloads.state_dict(wl.hidden, wl.intermediate, layer=0, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format=wl.fmt, max_tokens=wl.tokens)
+    x = workloads.activations(wl.tokens, wl.hidden, gain=wl.gain, device=cuda)
+    x4 = x.view(1, 1, wl.tokens, wl.hidden)
+    y32 = mlp.forward(x4, residual=x4, out_dtype=torch.float32)
+    y16 = mlp.forward(x4, residual=x4)
+    n32 = mlp.forward(x4, out_dtype=torch.float32)  # bare MLP output (the reference's forward(x))
+    n16 = mlp.forward(x4)
+    torch.cuda.synchronize()
+    assert tuple(y16.shape) == (1, 1, wl.tokens, wl.hidden) and y16.dtype == torch.bfloat16
+    # the bf16 output is exactly the fp32 output rounded once
+    assert torch.equal(y32.to(torch.bfloat16), y16) and torch.equal(n32.to(torch.bfloat16), n16)
+    hw = _host_weights(pkg, sd, wl.fmt)
+    xf = x.float().cpu().numpy()
+    ref, nref = _oracle(xf, hw), _oracle(xf, hw, residual=False)
+    _check(y32.reshape(wl.tokens, wl.hidden).cpu().numpy(), ref, name)
+    _check(n32.reshape(wl.tokens, wl.hidden).cpu().numpy(), nref, name + " (no residual)")
+    _check_bf16(y16.reshape(wl.tokens, wl.hidden).float().cpu().numpy(), ref, name)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+def test_forward_every_small_width(pkg, cuda, fmt):
+    import torch
+    from qwen_mlp_amd import workloads
+
+    H, I = 1024, 3072
+    sd = workloads.state_dict(H, I, layer=1, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=128)
+    hw = _host_weights(pkg, sd, fmt)
+    for M in list(range(1, 34)) + [47, 64, 100]:
+        x = workloads.activations(M, H, seed=3891 + M, device=cuda)
+        y = mlp.forward(x, residual=x, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        xf = x.float().cpu().numpy()
+        _check(y.cpu().numpy(), _oracle(xf, hw), f"{fmt} H={H} I={I} M={M}")
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+def test_zero_input_and_aliasing(pkg, cuda, fmt):
+    import torch
+    from qwen_mlp_amd import workloads
+
+    H, I = 1024, 3072
+    sd = workloads.state_dict(H, I, layer=2, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=16)
+    x = torch.zeros((5, H), dtype=torch.bfloat16, device=cuda)
+    r = workloads.activations(5, H, seed=5, device=cuda)
+    assert torch.equal(mlp.forward(x, residual=r), r)
+    assert not mlp.forward(x).float().abs().max().item()
+    # out may alias the residual (in-place residual stream update)
+    x = workloads.activations(5, H, seed=6, device=cuda)
+    expect = mlp.forward(x, residual=r)
+    rr = r.clone()
+    mlp.forward(x, residual=rr, out=rr)
+    assert torch.equal(rr, expect)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+def test_bitwise_deterministic(pkg, cuda, fmt):
+    import torch
+    from qwen_mlp_amd import workloads
+
+    H, I = 5120, 17408
+    sd = workloads.state_dict(H, I, layer=3, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=32)
+    for M in (1, 16, 32):
+        x = workloads.activations(M, H, seed=7391 + M, device=cuda)
+        a = mlp.forward(x, residual=x)
+        b = mlp.forward(x, residual=x)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+def test_graph_capture_replays(pkg, cuda, fmt):
+    import torch
+    from qwen_mlp_amd import workloads
+
+    H, I, M = 1024, 3072, 16
+    sd = workloads.state_dict(H, I, layer=4, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=M)
+    static_x = workloads.activations(M, H, seed=1, device=cuda)
+    static_out = torch.empty_like(static_x)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        mlp.forward(static_x, residual=static_x, out=static_out)  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        mlp.forward(static_x, residual=static_x, out=static_out)
+    for seed in range(5):
+        new_x = workloads.activations(M, H, seed=100 + seed, device=cuda)
+        static_x.copy_(new_x)
+        g.replay()
+        torch.cuda.synchronize()
+        eager = mlp.forward(new_x, residual=new_x)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager), f"replay {seed} differs from eager"
+
+
+def test_layer_chain(pkg, cuda):
+    """Four chained layers (residual stream) checked layer by layer against the oracle."""
+    import torch
+    from qwen_mlp_amd import workloads
+
+    H, I, M = 1024, 3072, 16
+    x = workloads.activations(M, H, seed=9, device=cuda)
+    for layer in range(4):
+        fmt = "bfp8" if layer % 2 else "bf16"
+        sd = workloads.state_dict(H, I, layer=10 + layer, device=cuda)
+        mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=M)
+        y = mlp.forward(x, residual=x)
+        torch.cuda.synchronize()
+        xf = x.float().cpu().numpy()
+        _check_bf16(y.float().cpu().numpy(), _oracle(xf, _host_weights(pkg, sd, fmt)), f"chain layer {layer} {fmt}")
+        x = y
+
+
+def test_shape_errors(pkg, cuda):
+    import torch
+    from qwen_mlp_amd import workloads
+
+    sd = workloads.state_dict(1024, 3072, layer=5, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format="bfp8", max_tokens=4)
+    with pytest.raises(ValueError):
+        mlp.forward(torch.zeros((2, 1000), dtype=torch.bfloat16, device=cuda))
+    with pytest.raises(ValueError):
+        mlp.forward(torch.zeros((2, 1024), dtype=torch.float32, device=cuda))
+    with pytest.raises(ValueError):
+        mlp.forward(torch.zeros((2, 1024), dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        pkg.pack_weight(torch.zeros((17, 256), dtype=torch.bfloat16, device=cuda))

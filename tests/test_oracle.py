@@ -1,0 +1,280 @@
+"""Pins for the CPU oracle (no GPU).  Each check is chosen so that a plausible slip -- a wrong tie
+rule, a dropped clamp, an off-by-one exponent, a transposed operand -- fails one of them."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import bf16, bfp8, c_oracle
+from oracle import mlp as omlp
+
+
+def _bf16_words(rng, shape, scale=1.0):
+    return bf16.f32_to_bits((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+# ---------------------------------------------------------------- bf16 rounding
+
+
+def test_rne_and_ties_away_over_every_finite_bin():
+    # Same enumeration as scripts/ci/test_mlp_rounding_policy.py:16-27.
+    uppers = np.arange(65536, dtype=np.uint32)
+    uppers = uppers[(uppers & 0x7F80) != 0x7F80]
+    for tail in (0, 0x7FFF, 0x8000, 0x8001, 0xFFFF):
+        words = (uppers << 16) | tail
+        vals = words.astype(np.uint32).view(np.float32)
+        nearest = bf16.f32_to_bits(vals).astype(np.int64)
+        away = bf16.f32_to_bits(vals, ties_away=True).astype(np.int64)
+        if tail == 0x8000:
+            even = (uppers % 2) == 0
+            assert np.array_equal(away[even], nearest[even] + 1)
+            assert np.array_equal(away[~even], nearest[~even])
+        else:
+            assert np.array_equal(away, nearest)
+
+
+def test_rne_matches_torch_cast():
+    torch = pytest.importorskip("torch")
+    rng = np.random.RandomState(11)
+    words = rng.randint(0, 2**32, size=200000, dtype=np.uint64).astype(np.uint32)
+    words = words[(words & 0x7F800000) != 0x7F800000]
+    vals = words.view(np.float32)
+    ours = bf16.f32_to_bits(vals)
+    ref = torch.from_numpy(vals.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, ref)
+    # the C oracle's rounding agrees too
+    for v in vals[:2000]:
+        assert c_oracle.f32_to_bf16_rne(v) == int(bf16.f32_to_bits(np.float32(v))[0])
+
+
+def test_double_rounding_known_answer():
+    # scripts/ci/test_mlp_c1e_pack.py:533-540: one rounding of silu(g)*u gives 0xBEBF, rounding the
+    # operands first gives 0xBEC0.
+    g = np.array([0xBFB582D0], dtype=np.uint32).view(np.float32)
+    u = np.array([0x3FAD03BC], dtype=np.uint32).view(np.float32)
+    s = omlp.silu(g)
+    assert int(bf16.f32_to_bits(s * u)[0]) == 0xBEBF
+    assert int(bf16.f32_to_bits(bf16.round_f32(s) * bf16.round_f32(u))[0]) == 0xBEC0
+
+
+def test_double_rounding_changes_a_large_share():
+    # scripts/ci/test_mlp_c1e_pack.py:524-530 (same distribution, numpy generator).
+    rng = np.random.RandomState(7)
+    gate = (rng.standard_normal(200000) * 1.43).astype(np.float32)
+    up = (rng.standard_normal(200000) * 1.43).astype(np.float32)
+    s = omlp.silu(gate)
+    fused = bf16.f32_to_bits(s * up)
+    separate = bf16.f32_to_bits(bf16.round_f32(s) * bf16.round_f32(up))
+    assert (fused != separate).mean() > 0.25
+
+
+# ---------------------------------------------------------------- bfp8 quantiser
+
+
+EDGE_WORDS = [
+    [0x0000] * 16,                                    # all zero -> e8 0
+    [0x8000] + [0x0000] * 15,                         # negative zero only
+    [0x7F7F] + [0x0001] * 15,                         # bf16 max with denormals
+    [0x0001, 0x8002, 0x0003] + [0x0000] * 13,         # denormals only (tiny group, e8 clamps to 1)
+    [0x3F80, 0x3F81, 0xBF80, 0x3B80] + [0x3C00] * 12, # 1.0 neighbourhood
+]
+
+
+def test_quantise_edge_words_numpy_vs_c():
+    words = np.array(EDGE_WORDS, dtype=np.uint16).reshape(len(EDGE_WORDS), 16)
+    q, e8 = bfp8.quantize(words)
+    qc, ec = c_oracle.quantize(words)
+    assert np.array_equal(q, qc) and np.array_equal(e8, ec)
+    assert e8[0, 0] == 0 and not q[0].any()
+    assert e8[1, 0] == 0 and not q[1].any()
+    # 0x7F7F = 255 * 2^120: frexp exponent 128 -> e8 248, 255/2 ties to 128 -> clamp 127
+    assert e8[2, 0] == 248 and q[2, 0] == 127
+    assert e8[3, 0] == 1  # denormal group: scale floor 2^-126
+
+
+@pytest.mark.parametrize("scale", [0.02, 1.0, 3e-5, 7e4])
+def test_quantise_numpy_matches_c(scale):
+    rng = np.random.RandomState(int(scale * 1000) % 997)
+    w = _bf16_words(rng, (48, 256), scale)
+    q, e8 = bfp8.quantize(w)
+    qc, ec = c_oracle.quantize(w)
+    assert np.array_equal(q, qc)
+    assert np.array_equal(e8, ec)
+    assert np.array_equal(bfp8.dequantize(q, e8), c_oracle.dequantize(q, e8))
+
+
+def test_dequantised_groups_are_block_float_exact():
+    # The reference's representability invariant (scripts/ci/ordered_cache_hw_plan.py:243-260).
+    rng = np.random.RandomState(3)
+    for scale in (0.02, 1.0, 1e-3):
+        w = _bf16_words(rng, (64, 512), scale)
+        q, e8 = bfp8.quantize(w)
+        assert bfp8.bf8_exact(bfp8.dequantize(q, e8))
+        assert np.abs(q.astype(np.int32)).max() <= 127
+
+
+def test_round_trip_exact_on_representable_groups():
+    rng = np.random.RandomState(5)
+    groups = 4096
+    q = rng.randint(-127, 128, size=(groups, 16))
+    q[:, 0] = np.where(rng.rand(groups) < 0.5, 1, -1) * rng.randint(64, 128, size=groups)  # max |q| in [64, 127]
+    E = rng.randint(-40, 40, size=groups)
+    v = (q * np.ldexp(1.0, (E - 7))[:, None]).astype(np.float32)
+    words = bf16.f32_to_bits(v)
+    assert np.array_equal(bf16.bits_to_f32(words), v)  # 7-bit integers times 2^k are exact in bf16
+    assert bfp8.bf8_exact(v)
+    qq, e8 = bfp8.quantize(words.reshape(groups // 4, 64))
+    assert np.array_equal(qq.reshape(groups, 16), q)
+    assert np.array_equal(e8.reshape(groups), (E + 120).astype(np.uint8))
+    assert np.array_equal(bfp8.dequantize(qq, e8).reshape(groups, 16), v)
+
+
+def test_brute_force_nearest_on_single_groups():
+    rng = np.random.RandomState(9)
+    for trial in range(300):
+        scale = 10.0 ** rng.uniform(-6, 4)
+        words = _bf16_words(rng, (1, 16), scale)
+        vals = [float(x) for x in bf16.bits_to_f32(words)[0]]
+        q, e8 = bfp8.quantize(words)
+        shared = max(math.frexp(v)[1] for v in vals if v != 0)
+        assert int(e8[0, 0]) == shared + 120
+        s = 2.0 ** (shared - 7)
+        for v, got in zip(vals, q[0]):
+            best = min(range(-127, 128), key=lambda c: (abs(v - c * s), c % 2))
+            assert int(got) == best, (trial, v, s, got, best)
+
+
+def test_error_is_at_most_half_a_step():
+    rng = np.random.RandomState(13)
+    w = _bf16_words(rng, (128, 1024), 0.02)
+    q, e8 = bfp8.quantize(w)
+    v = bf16.bits_to_f32(w).astype(np.float64).reshape(128, 64, 16)
+    d = bfp8.dequantize(q, e8).astype(np.float64).reshape(128, 64, 16)
+    step = np.ldexp(1.0, e8.astype(np.int64) - 127)[..., None]
+    clamped = np.abs(v) > 127.5 * step
+    err = np.abs(v - d)
+    assert (err[~clamped] <= step.repeat(16, axis=2)[~clamped] / 2).all()
+    assert (err[clamped] <= step.repeat(16, axis=2)[clamped]).all()
+
+
+def test_non_finite_weights_are_rejected():
+    w = np.zeros((1, 16), np.uint16)
+    w[0, 3] = 0x7F80
+    with pytest.raises(ValueError):
+        bfp8.quantize(w)
+    with pytest.raises(ValueError):
+        c_oracle.quantize(w)
+
+
+# ---------------------------------------------------------------- device tile layout (restated)
+
+
+def test_tiled_layout_is_a_bijection_and_lossless():
+    rng = np.random.RandomState(21)
+    rows, cols = 48, 768
+    w = _bf16_words(rng, (rows, cols), 0.02)
+    q, e8 = bfp8.quantize(w)
+    tiles, rowexp, flushed = bfp8.pack_tiles(q, e8)
+    assert flushed == 0
+    assert tiles.size + rows * 4 + bfp8.TRAILER_BYTES == bfp8.packed_bytes(rows, cols, "bfp8")
+    assert np.array_equal(bfp8.dequant_tiles(tiles, rowexp, rows, cols), bfp8.dequantize(q, e8))
+    # every mantissa byte appears exactly once
+    m = tiles.reshape(-1, bfp8.BLOCK_BYTES)[:, :4096].reshape(-1)
+    assert np.array_equal(np.sort(m.astype(np.int64) - 128), np.sort(q.reshape(-1).astype(np.int64)))
+    # bf16 tiles are a permutation of the words
+    tb = bfp8.pack_tiles_bf16(w).view(np.uint16)
+    assert np.array_equal(np.sort(tb), np.sort(w.reshape(-1)))
+
+
+def test_tiled_layout_reports_groups_outside_the_window():
+    rows, cols = 16, 256
+    w = np.zeros((rows, cols), np.float32)
+    w[:, :16] = 1.0
+    w[:, 16:32] = 2.0 ** -19   # 19 binades below: kept
+    w[:, 32:48] = 2.0 ** -20   # 20 binades below: outside the fp16 window
+    q, e8 = bfp8.quantize(bf16.f32_to_bits(w))
+    tiles, rowexp, flushed = bfp8.pack_tiles(q, e8)
+    assert flushed == rows
+    d = bfp8.dequant_tiles(tiles, rowexp, rows, cols)
+    assert (d[:, 16:32] == 2.0 ** -19).all() and (d[:, 32:48] == 0).all()
+
+
+# ---------------------------------------------------------------- SwiGLU formula
+
+
+def _brute(x, wg, wu, wd, res):
+    M, H = x.shape
+    I = wg.shape[0]
+    out = np.zeros((M, H))
+    for m in range(M):
+        h = []
+        for n in range(I):
+            g = sum(float(x[m, k]) * float(wg[n, k]) for k in range(H))
+            u = sum(float(x[m, k]) * float(wu[n, k]) for k in range(H))
+            h.append(g / (1.0 + math.exp(-g)) * u)
+        for n in range(H):
+            out[m, n] = float(res[m, n]) + sum(h[k] * float(wd[n, k]) for k in range(I))
+    return out
+
+
+def _small(seed, M=3, H=32, I=48):
+    rng = np.random.RandomState(seed)
+    x = rng.standard_normal((M, H)).astype(np.float32)
+    wg = (rng.standard_normal((I, H)) * 0.3).astype(np.float32)
+    wu = (rng.standard_normal((I, H)) * 0.3).astype(np.float32)
+    wd = (rng.standard_normal((H, I)) * 0.3).astype(np.float32)
+    res = rng.standard_normal((M, H)).astype(np.float32)
+    return x, wg, wu, wd, res
+
+
+def test_swiglu_matches_float64_brute_force():
+    x, wg, wu, wd, res = _small(1)
+    got = omlp.swiglu(x, wg, wu, wd, residual=res)
+    ref = _brute(x, wg, wu, wd, res)
+    assert np.allclose(got, ref, rtol=2e-5, atol=2e-5)
+
+
+def test_swiglu_matches_c_oracle_and_torch_float64():
+    torch = pytest.importorskip("torch")
+    x, wg, wu, wd, res = _small(2, M=5, H=64, I=96)
+    got = omlp.swiglu(x, wg, wu, wd, residual=res)
+    assert np.allclose(c_oracle.swiglu(x, wg, wu, wd, residual=res), got, rtol=1e-5, atol=1e-5)
+    t = [torch.from_numpy(a).double() for a in (x, wg, wu, wd, res)]
+    ref = (torch.nn.functional.silu(t[0] @ t[1].T) * (t[0] @ t[2].T)) @ t[3].T + t[4]
+    assert np.allclose(got, ref.numpy(), rtol=1e-5, atol=1e-5)
+    # the torch-float32 restatement used for the CPU baseline is the same formula
+    tt = [torch.from_numpy(a) for a in (x, wg, wu, wd, res)]
+    assert np.allclose(omlp.swiglu_torch(*tt[:4], residual=tt[4]).numpy(), got, rtol=1e-5, atol=1e-5)
+
+
+def test_swiglu_zero_input_returns_residual():
+    x, wg, wu, wd, res = _small(3)
+    assert np.array_equal(omlp.swiglu(np.zeros_like(x), wg, wu, wd, residual=res), res)
+
+
+def test_swiglu_is_exactly_linear_in_the_down_weight():
+    x, wg, wu, wd, _ = _small(4)
+    a = omlp.swiglu(x, wg, wu, wd)
+    b = omlp.swiglu(x, wg, wu, 2.0 * wd)
+    assert np.array_equal(b, 2.0 * a)
+
+
+def test_swiglu_gate_and_up_are_not_interchangeable():
+    # a transposed/swapped operand must show: silu is applied to the gate only
+    x, wg, wu, wd, _ = _small(5)
+    assert not np.allclose(omlp.swiglu(x, wg, wu, wd), omlp.swiglu(x, wu, wg, wd), atol=1e-3)
+
+
+def test_swiglu_is_invariant_under_intermediate_permutation():
+    x, wg, wu, wd, res = _small(6)
+    perm = np.random.RandomState(0).permutation(wg.shape[0])
+    a = omlp.swiglu(x, wg, wu, wd, residual=res)
+    b = omlp.swiglu(x, wg[perm], wu[perm], wd[:, perm], residual=res)
+    assert np.allclose(a, b, rtol=1e-5, atol=1e-5)
+
+
+def test_tolerance_helper():
+    ok, err, bound = omlp.tolerance_ok(np.array([1.0, 2.0]), np.array([1.0, 2.01]))
+    assert ok and abs(err - 0.01) < 1e-12 and abs(bound - 1e-2 * math.sqrt((1 + 2.01**2) / 2)) < 1e-12
+    ok, _, _ = omlp.tolerance_ok(np.array([1.0, 2.1]), np.array([1.0, 2.0]))
+    assert not ok
