@@ -1,0 +1,268 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused Qwen3 SwiGLU MLP on one MI355X.
+
+One step = one MLP layer ``out = x + down(silu(gate(x)) * up(x))`` at the Qwen3-27B shape
+(hidden 5120, intermediate 17408) over M = 16 tokens (a speculative-verify block), bfp8 weights
+(16-value groups sharing an 8-bit exponent), inputs resident in HBM.  Steps rotate over several
+independently seeded layers so that no weight byte is served from L2 or the 256 MB last-level
+cache.  The timed region is bracketed by device synchronisation; per-kernel HIP events recorded
+on the forward's stream time the dominant (gate/up) kernel inside the same region.
+
+Prints one JSON line: metric, value (achieved HBM GB/s of the whole layer, algorithmic bytes
+W + 4*M*H), ms_per_step, the gate/up kernel's roofline, the CPU baseline (the oracle's torch fp32
+formula on this host's cores) and, unless --no-extras, the bf16-weight variant, the M = 1/32
+sweep, a 64-layer stack and the M = 2048 prefill chunk.
+"""
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+METRIC = "fused MLP µs/layer + achieved HBM GB/s (% of peak) at M=16, 27B shape, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="qwen3-27b-mlp-m16-bfp8")
+    ap.add_argument("--rotate", type=int, default=8, help="distinct layers cycled through by the timed loop")
+    ap.add_argument("--no-extras", action="store_true", help="skip the bf16 variant, sweep, stack and prefill")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def make_layers(pkg, workloads, wl, n, device, first_layer=0):
+    layers = []
+    for i in range(n):
+        sd = workloads.state_dict(wl.hidden, wl.intermediate, layer=first_layer + i, device=device)
+        layers.append(pkg.load_mlp_weights(device, sd, weight_format=wl.fmt))
+        del sd
+    return layers
+
+
+def time_layers(pkg, layers, x, steps, warmup, profile=False, chain=False):
+    """Runs `steps` forwards cycling through `layers`; returns (ms_per_step, kernel_ms dict)."""
+    import torch
+
+    lib = pkg.lib()
+    M, H = x.shape
+    I = layers[0].intermediate
+    ws = pkg.new_workspace(M, H, I, layers[0].fmt, x.device)
+    outs = [torch.empty_like(x), torch.empty_like(x)]
+    for i in range(warmup):
+        pkg.mlp_forward(x, layers[i % len(layers)], residual=x, out=outs[i % 2], workspace=ws)
+    events = []
+    if profile:
+        for _ in range(steps):
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            for e in evs:
+                e.record()  # materialise the handle
+            events.append(evs)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cur = x
+    start.record()
+    for i in range(steps):
+        if profile:
+            arr = (__import__("ctypes").c_void_p * 4)(*[e._as_parameter_.value for e in events[i]])
+            lib.qmlp_set_profile_events(arr, 4)
+        out = outs[i % 2]
+        pkg.mlp_forward(cur, layers[i % len(layers)], residual=cur, out=out, workspace=ws)
+        if chain:
+            cur = out
+    if profile:
+        lib.qmlp_set_profile_events(None, 0)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    kern = {}
+    if profile:
+        names = ("prep", "gate_up", "down")
+        for k, name in enumerate(names):
+            kern[name] = statistics.fmean(ev[k].elapsed_time(ev[k + 1]) for ev in events)
+    return ms, kern
+
+
+def cpu_baseline(pkg, workloads, wl, device, seconds):
+    """The oracle's restatement of the reference CPU path (torch fp32 formula,
+    scripts/ci/mlp-sweep.py:121-126) on identically dequantised weights, this host's cores."""
+    import numpy as np
+    import torch
+
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    from oracle import bfp8 as obfp8
+    from oracle import mlp as omlp
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    sd = workloads.state_dict(wl.hidden, wl.intermediate, layer=0, device=device)
+    w = {}
+    for name in ("gate_proj", "up_proj", "down_proj"):
+        t = sd[f"{name}.weight"]
+        if wl.fmt == "bfp8":
+            q, e8 = pkg.quantize_bfp8(t)
+            w[name] = torch.from_numpy(obfp8.dequantize(q.cpu().numpy(), e8.cpu().numpy()))
+        else:
+            w[name] = t.float().cpu()
+    del sd
+    x = workloads.activations(wl.tokens, wl.hidden, gain=wl.gain, device=device).float().cpu()
+    omlp.swiglu_torch(x, w["gate_proj"], w["up_proj"], w["down_proj"], residual=x)  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < 5 or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        omlp.swiglu_torch(x, w["gate_proj"], w["up_proj"], w["down_proj"], residual=x)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 2000:
+            break
+    med = statistics.median(times)
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(wl.algorithmic_bytes() / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(times)} single-layer forwards of the same workload (median), torch fp32 on "
+                  f"dequantised weights, {threads} threads, os.cpu_count()={os.cpu_count()}, {cpu_model}",
+        "us_per_layer": round(med * 1e6, 1),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build runs the unsharded MLP on a single MI355X; "
+              f"--gpus {args.gpus} (WORLD_SIZE={world}) is not supported.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    sys.path.insert(0, ROOT)
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    from qwen_mlp_amd import workloads
+
+    dev = torch.device("cuda:0")
+    wl = workloads.WORKLOADS[args.workload]
+    _log(f"workload {wl.name}: generating {args.rotate} layers")
+    layers = make_layers(pkg, workloads, wl, args.rotate, dev)
+    x = workloads.activations(wl.tokens, wl.hidden, gain=wl.gain, device=dev)
+    _log(f"timing {args.steps} steps after {args.warmup} warm-up")
+    ms, kern = time_layers(pkg, layers, x, args.steps, args.warmup, profile=True)
+    layer_bytes = wl.algorithmic_bytes()
+    value = layer_bytes / (ms / 1e3) / 1e9
+    per = 17 / 16 if wl.fmt == "bfp8" else 2
+    gu_bytes = int(2 * wl.hidden * wl.intermediate * per + 2 * wl.tokens * wl.hidden)
+    gu_ms = kern["gate_up"]
+    gu_gbs = gu_bytes / (gu_ms / 1e3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gate_up_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tinfo = json.load(f)
+        if tinfo.get("workload") == wl.name:
+            traffic = tinfo.get("hbm_bytes_per_launch")
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_layer": round(ms * 1e3, 2),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16-mfma/f32-acc (bfp8 weights)" if wl.fmt == "bfp8" else "bf16-mfma/f32-acc",
+        "data": "synthetic: x ~ N(0,1)*U(0.5,1.5) gain, random-init weights N(0,0.02), seeds 1000/2000+",
+        "config": {"workload": wl.name, "hidden": wl.hidden, "intermediate": wl.intermediate,
+                   "tokens": wl.tokens, "weight_format": wl.fmt, "layers_rotated": args.rotate,
+                   "algorithmic_bytes_per_layer": layer_bytes},
+        "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
+        "roofline": {"kernel": "gate_up (skinny_kernel, 2 matrices)", "bound": "hbm",
+                     "achieved": round(gu_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": gu_bytes},
+    }
+    del layers
+    torch.cuda.empty_cache()
+    if not args.no_extras:
+        extras = {}
+        # bf16-weight variant of the same layer (the 2x comparison)
+        if wl.fmt == "bfp8":
+            wb = workloads.Workload(wl.name.replace("bfp8", "bf16"), wl.hidden, wl.intermediate, wl.tokens, "bf16",
+                                    wl.gain)
+            _log("bf16-weight variant")
+            lb = make_layers(pkg, workloads, wb, max(4, args.rotate // 2), dev)
+            msb, _ = time_layers(pkg, lb, x, max(50, args.steps // 2), 10)
+            del lb
+            torch.cuda.empty_cache()
+            extras["bf16_variant"] = {"us_per_layer": round(msb * 1e3, 2),
+                                      "gbs": round(wb.algorithmic_bytes() / (msb / 1e3) / 1e9, 2),
+                                      "bfp8_speedup": round(msb / ms, 3)}
+            # width sweep
+            sweep = {}
+            lq = make_layers(pkg, workloads, wl, args.rotate, dev)
+            for M in (1, 32):
+                xm = workloads.activations(M, wl.hidden, gain=wl.gain, device=dev)
+                msm, km = time_layers(pkg, lq, xm, max(50, args.steps // 2), 10, profile=True)
+                b = wl.weight_bytes() + 4 * M * wl.hidden
+                sweep[f"M={M}"] = {"us_per_layer": round(msm * 1e3, 2), "gbs": round(b / (msm / 1e3) / 1e9, 2),
+                                   "pct_hbm_peak": round(100 * b / (msm / 1e3) / 1e9 / HBM_PEAK_GBS, 2)}
+            extras["width_sweep"] = sweep
+            del lq
+            torch.cuda.empty_cache()
+            # 64-layer stack, chained through the residual stream
+            _log("64-layer stack")
+            stack = make_layers(pkg, workloads, wl, 64, dev, first_layer=100)
+            mss, _ = time_layers(pkg, stack, x, 128, 64, chain=True)
+            extras["stack64"] = {"layers": 64, "bytes": 64 * wl.algorithmic_bytes(),
+                                 "ms_per_stack": round(mss * 64, 4), "us_per_layer": round(mss * 1e3, 2),
+                                 "sustained_gbs": round(wl.algorithmic_bytes() / (mss / 1e3) / 1e9, 2)}
+            del stack
+            torch.cuda.empty_cache()
+            # prefill chunk
+            _log("prefill M=2048")
+            wp = workloads.WORKLOADS["qwen3-27b-mlp-prefill-m2048-bfp8"]
+            lp = make_layers(pkg, workloads, wp, 2, dev)
+            xp = workloads.activations(wp.tokens, wp.hidden, gain=False, device=dev)
+            msp, _ = time_layers(pkg, lp, xp, 10, 2)
+            tflops = wp.flops() / (msp / 1e3) / 1e12
+            extras["prefill_m2048"] = {"us_per_layer": round(msp * 1e3, 1), "tflops": round(tflops, 1),
+                                       "mfma_util_vs_bf16_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
+            del lp
+            torch.cuda.empty_cache()
+        result["extras"] = extras
+    if not args.no_cpu:
+        _log("CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(pkg, workloads, wl, dev, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -129,6 +129,16 @@ size_t qmlp_workspace_bytes(int M, int H, int I, int fmt);
 /* Zero-fills the workspace with a kernel (not a memset node, so it may be graph-captured). */
 int qmlp_workspace_init(void* ws, size_t ws_bytes, qmlp_stream_t stream);
 
+/* ---------------------------------------------------------------- profiling (host only)
+ *
+ * Per-kernel timing of the forward pass, the counterpart of the reference's per-op signposts
+ * (docker/qwen-c2-graft/graft/layer.py:18-90).  When n == 4, every later qmlp_forward on this host
+ * thread records events[0] before its first kernel, events[1] after the activation prep (bfp8;
+ * == events[0] for bf16), events[2] after the gate/up kernel and events[3] after the down kernel,
+ * on the forward's stream (hipEvent_t handles).  n == 0 turns recording off.  Only the
+ * weight-streaming path (M <= 32) records. */
+int qmlp_set_profile_events(void* const* events, int n);
+
 /* ---------------------------------------------------------------- planning (host only)
  *
  * Work split of one weight-streaming projection: `rows` output rows (multiple of 16) over K
@@ -137,6 +147,12 @@ int qmlp_workspace_init(void* ws, size_t ws_bytes, qmlp_stream_t stream);
  * coverage of the split can be tested without a GPU, like the reference's worker-to-pair mapping
  * tests (scripts/ci/test_fused_1d.py:71-79). */
 int qmlp_plan_skinny(int rows, int K, int M, int num_cus, int* out4);
+
+/* Work split of the M <= 16 kernel for one projection with `nmat` matrices (2 = gate/up,
+ * 1 = down): the (16-row tile x 256-K superblock) grid cut into tile groups x K splits.
+ * Fills out[0..5] = {workgroups, tiles per group, K splits, superblocks per split, groups,
+ * tiles one wave may touch}. */
+int qmlp_plan_split(int rows, int K, int nmat, int num_cus, int* out6);
 
 #ifdef __cplusplus
 }

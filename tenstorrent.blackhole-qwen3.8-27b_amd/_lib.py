@@ -35,6 +35,8 @@ SIGNATURES = {
     "qmlp_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "qmlp_workspace_init": (_I, [_P, _SZ, _P]),
     "qmlp_plan_skinny": (_I, [_I, _I, _I, _I, ctypes.POINTER(ctypes.c_int)]),
+    "qmlp_set_profile_events": (_I, [_P, _I]),
+    "qmlp_plan_split": (_I, [_I, _I, _I, _I, ctypes.POINTER(ctypes.c_int)]),
 }
 
 _lib = None

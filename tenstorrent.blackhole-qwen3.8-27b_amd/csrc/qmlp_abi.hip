@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "../../include/qwen_mlp.h"
@@ -28,12 +29,25 @@ int check_launch(const char* what) {
   return 0;
 }
 
+static thread_local hipEvent_t g_prof[4];
+static thread_local bool g_prof_on = false;
+
+void set_profile_events(const hipEvent_t* ev) {
+  g_prof_on = ev != nullptr;
+  if (ev)
+    for (int i = 0; i < 4; ++i) g_prof[i] = ev[i];
+}
+
+void profile_mark(int i, hipStream_t s) {
+  if (g_prof_on) (void)hipEventRecord(g_prof[i], s);
+}
+
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 WsLayout ws_layout(int M, int H, int I, int fmt) {
   WsLayout L{};
   size_t off = 0;
-  L.counters_gu = off;
+  L.counters_gu = off;  // per tile (stream-K) or per tile group (split kernel): <= tiles
   off = align256(off + (size_t)(I / kTileRows) * 4);
   L.counters_d = off;
   off = align256(off + (size_t)(H / kTileRows) * 4);
@@ -45,10 +59,19 @@ WsLayout ws_layout(int M, int H, int I, int fmt) {
   off = align256(off + (fmt == QMLP_FMT_BFP8 ? (size_t)M * H * 2 : 0));
   L.h = off;
   off = align256(off + (size_t)M * I * 2);
-  L.part_gu = off;  // 2 slots per workgroup, 2 matrices x 2 column tiles x 64 lanes x 16 B
-  off = align256(off + (size_t)2 * kMaxWorkgroups * (2 * 2 * 64 * 16));
+  // partial-sum slots: the stream-K kernel (M > 16) needs 2 slots per workgroup of
+  // 2 matrices x 2 column tiles x 64 lanes x 16 B; the split kernel (M <= 16) one slot per
+  // (workgroup, tile) of NMAT x 64 lanes x 16 B.
+  const size_t sk_gu = (size_t)2 * kMaxWorkgroups * (2 * 2 * 64 * 16);
+  const size_t sk_d = (size_t)2 * kMaxWorkgroups * (1 * 2 * 64 * 16);
+  const size_t gv_gu = gemv_max_slots(I, H, 2) * (2 * 64 * 16);
+  const size_t gv_d = gemv_max_slots(H, I, 1) * (1 * 64 * 16);
+  L.part_gu = off;
+  off = align256(off + std::max(sk_gu, gv_gu));
   L.part_d = off;
-  off = align256(off + (size_t)2 * kMaxWorkgroups * (1 * 2 * 64 * 16));
+  off = align256(off + std::max(sk_d, gv_d));
+  L.pss = off;
+  off = align256(off + (size_t)kMaxWorkgroups * 16 * 4);
   L.total = off;
   return L;
 }
@@ -212,12 +235,36 @@ int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* w
   if (int rc = current_device_info(&di)) return rc;
   ForwardArgs a{x, (const uint8_t*)wg, (const uint8_t*)wu, (const uint8_t*)wd, residual, out, (uint8_t*)ws,
                 M, H, I, fmt, (flags & QMLP_OUT_F32) ? 1 : 0, (flags & QMLP_RESIDUAL_F32) ? 1 : 0};
+  if (gemv_supported(M, H, I, di.num_cus)) return launch_forward_gemv(a, di.num_cus, (hipStream_t)stream);
   return launch_forward_skinny(a, di.num_cus, (hipStream_t)stream);
 }
 
 int qmlp_forward(const void* x, const void* wg, const void* wu, const void* wd, const void* residual, void* out,
                  void* ws, size_t ws_bytes, int M, int H, int I, int fmt, qmlp_stream_t stream) {
   return qmlp_forward_ex(x, wg, wu, wd, residual, out, ws, ws_bytes, M, H, I, fmt, 0, stream);
+}
+
+int qmlp_set_profile_events(void* const* events, int n) {
+  if (n == 0) {
+    set_profile_events(nullptr);
+    return 0;
+  }
+  if (n != 4 || !events) return set_error(QMLP_E_SHAPE, "qmlp_set_profile_events: need 4 events or 0");
+  set_profile_events((hipEvent_t const*)events);
+  return 0;
+}
+
+int qmlp_plan_split(int rows, int K, int nmat, int num_cus, int* out6) {
+  if (!out6) return set_error(QMLP_E_NULL, "qmlp_plan_split: null pointer");
+  GemvPlan p;
+  if (plan_gemv(rows, K, nmat, num_cus, &p)) return set_error(QMLP_E_SHAPE, "qmlp_plan_split: no split for %dx%d", rows, K);
+  out6[0] = p.P;
+  out6[1] = p.G;
+  out6[2] = p.S;
+  out6[3] = p.KQ;
+  out6[4] = p.Ng;
+  out6[5] = p.maxseg;
+  return 0;
 }
 
 int qmlp_plan_skinny(int rows, int K, int M, int num_cus, int* out4) {

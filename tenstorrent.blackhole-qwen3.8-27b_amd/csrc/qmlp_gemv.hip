@@ -1,0 +1,636 @@
+// qmlp_gemv.hip -- weight-streaming kernels for M <= 16 tokens (decode / speculative verify).
+//
+// Reference realisation being replaced: FusedProjection (scripts/ci/fused_1d.py:96-196: 91
+// workers x 3 gate/up tile pairs, activation multicast fused_1d_input.cpp:1-51, weight reader
+// fused_1d_weights.cpp:1-44, SiLU*mul epilogue) followed by the widened down projection
+// (scripts/ci/mlp_down_grid.py:4-12).
+//
+// Work split.  A projection W[N, K] is T = N/16 row tiles x C = K/256 superblocks of 256 K values.
+// The (tile, superblock) grid is cut into Ng tile groups (G tiles each) x S K-splits (KQ = C/S
+// superblocks each), one workgroup per rectangle, P = Ng * S ~ #CUs workgroups with (nearly)
+// equal work.  At the Qwen3-27B shape both projections split exactly: gate/up 64 groups of 17
+// tiles x 4 quarters of 5 superblocks, down 64 groups of 5 tiles x 4 quarters of 17 superblocks,
+// 256 workgroups of 85 units each.
+//
+// Inside a workgroup:
+//   1. the token activations of its K range are staged once into LDS in the matrix-core B
+//      operand order (bfp8: converted bf16 -> fp16 with a per-(token, K range) power of two);
+//   2. the 8 waves split the rectangle's units (tile-major) into equal contiguous ranges and
+//      stream their weight blocks (ping-pong register stages, non-temporal 16-byte loads),
+//      dequantising in registers; partial sums are parked in LDS at tile boundaries;
+//   3. after one barrier each tile's partials are summed in wave order and published to a
+//      workspace slot; one release fence + one arrival counter per workgroup;
+//   4. the last of the S workgroups of a tile group sums the S slots in K order (deterministic)
+//      and runs the epilogue: gate/up -> h = silu(g) * u (bf16, or fp16 * 2^th for bfp8),
+//      down -> out = residual + y (bf16 or fp32).  It resets the counter for the next call.
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "qmlp_common.h"
+#include "qmlp_internal.h"
+
+namespace qmlp {
+
+struct GvParams {
+  const uint8_t* w0;
+  const uint8_t* w1;
+  const int* rowexp0;
+  const int* rowexp1;
+  const uint16_t* src;  // activations [M, K] row-major: x (bf16) for gate/up, h for down
+  int M, K, N;
+  int C, T, G, S, KQ, Ng, P, maxseg;
+  int x_scale;            // 1: src is bf16 and is converted to fp16 * 2^t (bfp8 gate/up)
+  const int* th_in;       // bfp8 down: h = h16 * 2^-th[m]
+  int* th_out;            // bfp8 gate/up: th[m] written by tile group 0
+  const Trailer* tg;      // bfp8 gate/up: weight row-norm trailers for the h bound
+  const Trailer* tu;
+  void* out;              // gate/up: h [M, N] 16-bit; down: out [M, N] bf16 or fp32
+  const void* residual;   // down: [M, N] bf16 or fp32, may alias out
+  int out_f32, res_f32;
+  float* part;            // [P][G][NMAT * 64] f32x4 partial slots
+  float* pss;             // [P][16] per-workgroup token sum of squares (bfp8 gate/up)
+  int* counters;          // [Ng] arrival counters (left at zero)
+};
+
+template <int WF, int NMAT, int SPS>
+struct GStage {
+  u32x4 w[NMAT][SPS][WF ? 1 : 2];
+  uint32_t e[NMAT];
+};
+
+// ---------------------------------------------------------------- staging of the B operand
+//
+// LDS layout: for each K-step kk of the workgroup's K range, 64 lanes x 32 bytes: lane
+// l = 16 * quarter + m holds the 16 values K = 64 kk + 16 quarter + (0..15) of token row m, so the
+// main loop reads its B operand with two conflict-free 16-byte LDS loads per K-step.
+//
+// Staging is split in two so that the activation loads are issued before the first weight
+// loads (vector loads complete in order: waiting for activations issued after the weights would
+// also wait for the weights).  Thread (m = token row, tl) handles chunks of 8 values at
+// K = 8 * (tl + c * TPR), c < nch = KQ; all MAXCH loads are unconditional (clamped chunk index).
+template <int NW, int MAXCH>
+struct BStage {
+  u32x4 v[MAXCH];
+};
+
+template <int NW, int MAXCH>
+__device__ __forceinline__ void stage_b_issue(const GvParams& p, int k0, BStage<NW, MAXCH>& bs) {
+  constexpr int TPR = NW * 64 / 16;  // threads per token row
+  const int m = threadIdx.x / TPR, tl = threadIdx.x % TPR;
+  const int mr = min(m, p.M - 1);  // rows beyond M duplicate row M-1 (their outputs are discarded)
+  const int nch = p.KQ * kSuperK / (TPR * 8);
+  const uint16_t* row = p.src + (size_t)mr * p.K + k0;
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) bs.v[c] = *(const u32x4*)(row + (tl + min(c, nch - 1) * TPR) * 8);
+}
+
+template <int NW, int MAXCH>
+__device__ __forceinline__ void stage_b_finish(const GvParams& p, const BStage<NW, MAXCH>& bs, uint8_t* ldsb,
+                                               int* lds_t, float* lds_ss) {
+  constexpr int TPR = NW * 64 / 16;
+  const int m = threadIdx.x / TPR, tl = threadIdx.x % TPR;
+  const int nch = p.KQ * kSuperK / (TPR * 8);
+  auto lds_off = [&](int e) {
+    const int kk = e >> 6, r = e & 63;
+    const int l = (r >> 4) * 16 + m;
+    return ((kk * 64 + l) * 2 + ((r >> 3) & 1)) * 16;
+  };
+  if (!p.x_scale) {
+#pragma unroll
+    for (int c = 0; c < MAXCH; ++c)
+      if (c < nch) *(u32x4*)(ldsb + lds_off((tl + c * TPR) * 8)) = bs.v[c];
+    return;
+  }
+  // bf16 -> fp16 * 2^t with max|x| * 2^t in [2^14, 2^15) over this K range (exact unless a value
+  // is 2^31 times smaller than the range maximum).  Also the range's sum of squares for th.
+  float mx = 0.f, ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {
+    if (c < nch) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = bf16_to_f32((uint16_t)(bs.v[c][i] & 0xffffu)), b = bf16_to_f32((uint16_t)(bs.v[c][i] >> 16));
+        mx = fmaxf(mx, fmaxf(fabsf(a), fabsf(b)));
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+    }
+  }
+  // reduce over the TPR threads of this row (a fixed tree inside one wave: deterministic)
+#pragma unroll
+  for (int o = TPR / 2; o > 0; o >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, o));
+    ss += __shfl_xor(ss, o);
+  }
+  int e2 = 0;
+  if (mx > 0.f) frexpf(mx, &e2);
+  const int t = mx > 0.f ? 15 - e2 : 0;
+  if (tl == 0) {
+    lds_t[m] = t;
+    lds_ss[m] = ss;
+  }
+#pragma unroll
+  for (int c = 0; c < MAXCH; ++c) {
+    if (c < nch) {
+      uint32_t o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = __builtin_amdgcn_ldexpf(bf16_to_f32((uint16_t)(bs.v[c][i] & 0xffffu)), t);
+        const float b = __builtin_amdgcn_ldexpf(bf16_to_f32((uint16_t)(bs.v[c][i] >> 16)), t);
+        o[i] = (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+      }
+      *(u32x4*)(ldsb + lds_off((tl + c * TPR) * 8)) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+}
+
+// Partial sums cross workgroups (and XCDs) through agent-scope relaxed atomic stores and loads:
+// they are coherent at the device level by themselves, so publishing needs no L2 write-back and
+// reading no L2 invalidation -- only the wait for the stores before the arrival counter moves.
+__device__ __forceinline__ void store_agent(float* p, f32x4 v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) __hip_atomic_store(p + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 load_agent(const float* p) {
+  f32x4 v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return v;
+}
+
+// ---------------------------------------------------------------- main loop pieces
+
+struct GPos {
+  int unit, part, tl, s;  // unit within the rectangle, stage part, tile (local), superblock (local)
+};
+
+template <int SPU>
+__device__ __forceinline__ void gadvance(GPos& q, int KQ) {
+  if (++q.part == SPU) {
+    q.part = 0;
+    ++q.unit;
+    if (++q.s == KQ) {
+      q.s = 0;
+      ++q.tl;
+    }
+  }
+}
+
+template <int WF, int NMAT, int SPS>
+__device__ __forceinline__ void gload(GStage<WF, NMAT, SPS>& st, const GvParams& p, size_t blk_base, const GPos& q,
+                                      uint32_t lw, uint32_t le) {
+  constexpr int BLK = WF ? kBfp8Block : kBf16Block;
+  const size_t blk = (blk_base + (size_t)q.tl * p.C + q.s) * BLK;
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat) {
+    const uint8_t* b = (mat ? p.w1 : p.w0) + blk;
+    const uint8_t* bp = b + q.part * SPS * (WF ? 1024 : 2048);
+#pragma unroll
+    for (int jj = 0; jj < SPS; ++jj) {
+      if constexpr (WF) {
+        st.w[mat][jj][0] = ld_stream((const u32x4*)(bp + lw + jj * 1024));
+      } else {
+        st.w[mat][jj][0] = ld_stream((const u32x4*)(bp + lw + jj * 2048));
+        st.w[mat][jj][1] = ld_stream((const u32x4*)(bp + lw + jj * 2048 + 1024));
+      }
+    }
+    if constexpr (WF) st.e[mat] = ld_stream((const uint32_t*)(b + le));
+  }
+}
+
+template <int WF, int NMAT, int SPS>
+__device__ __forceinline__ void gcompute(const GStage<WF, NMAT, SPS>& st, const GPos& q, const uint8_t* ldsb,
+                                         int lane, f32x4 (&acc)[NMAT][2]) {
+#pragma unroll
+  for (int jj = 0; jj < SPS; ++jj) {
+    const int j = q.part * SPS + jj;
+    const uint8_t* bp = ldsb + ((q.s * kSteps + j) * 64 + lane) * 32;
+    const u32x4 b0 = *(const u32x4*)bp;
+    const u32x4 b1 = *(const u32x4*)(bp + 16);
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) {
+      if constexpr (WF) {
+        f16x8 a0, a1;
+        dq16(st.w[mat][jj][0], scale_pair(st.e[mat], j), a0, a1);
+        acc[mat][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, b0), acc[mat][0], 0, 0, 0);
+        acc[mat][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, b1), acc[mat][1], 0, 0, 0);
+      } else {
+        acc[mat][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.w[mat][jj][0]),
+                                                              __builtin_bit_cast(bf16x8, b0), acc[mat][0], 0, 0, 0);
+        acc[mat][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.w[mat][jj][1]),
+                                                              __builtin_bit_cast(bf16x8, b1), acc[mat][1], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- epilogue (last arrival)
+//
+// Lane l holds rows 4*(l/16) + v (v = 0..3) of token column m = l % 16 -- the 16x16 matrix-core
+// output layout.
+template <int WF, int NMAT>
+__device__ __forceinline__ void gepilogue(const GvParams& p, int t, const f32x4 (&tot)[NMAT], int lane, int th) {
+  const int m = lane & 15;
+  if (m >= p.M) return;
+  const int nb = t * kTileRows + (lane >> 4) * 4;
+  uint16_t o[4];
+  if constexpr (NMAT == 2) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float g = tot[0][v], u = tot[1][v];
+      if constexpr (WF) {
+        g = __builtin_amdgcn_ldexpf(g, p.rowexp0[nb + v]);
+        u = __builtin_amdgcn_ldexpf(u, p.rowexp1[nb + v]);
+      }
+      const float hv = g / (1.0f + expf(-g)) * u;
+      // bf16 weights: h is the bf16 operand of the down projection, rounded once like the
+      // reference's fused epilogue; bfp8: fp16 * 2^th (one rounding from fp32).
+      o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(hv, th)) : f32_to_bf16(hv);
+    }
+  } else {
+    float y[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      y[v] = tot[0][v];
+      if constexpr (WF) y[v] = __builtin_amdgcn_ldexpf(y[v], p.rowexp0[nb + v] - p.th_in[m]);
+    }
+    if (p.residual) {
+      if (p.res_f32) {
+        const f32x4 r = *(const f32x4*)((const float*)p.residual + (size_t)m * p.N + nb);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) y[v] += r[v];
+      } else {
+        const u32x2 r = *(const u32x2*)((const uint16_t*)p.residual + (size_t)m * p.N + nb);
+        y[0] += bf16_to_f32((uint16_t)(r.x & 0xffffu));
+        y[1] += bf16_to_f32((uint16_t)(r.x >> 16));
+        y[2] += bf16_to_f32((uint16_t)(r.y & 0xffffu));
+        y[3] += bf16_to_f32((uint16_t)(r.y >> 16));
+      }
+    }
+    if (p.out_f32) {
+      *(f32x4*)((float*)p.out + (size_t)m * p.N + nb) = f32x4{y[0], y[1], y[2], y[3]};
+      return;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(y[v]);
+  }
+  *(u32x2*)((uint16_t*)p.out + (size_t)m * p.N + nb) =
+      u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+}
+
+// ---------------------------------------------------------------- kernel
+
+template <int WF, int NMAT, int NW, int MAXCH>
+__global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
+  constexpr int SPS = WF ? 4 : 2;  // K-steps per register stage
+  constexpr int SPU = kSteps / SPS;
+  constexpr int SLOT = NMAT * 64;  // f32x4 per parked partial
+  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ int s_t[16];
+  __shared__ float s_ss[16];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int w = xcd_logical(blockIdx.x, p.P);
+  const int g = w / p.S, q = w % p.S;
+  const int Gw = min(p.G, p.T - g * p.G);  // tiles in this group
+  const int U = Gw * p.KQ;
+  const int ua = (int)((long)wave * U / NW), ub = (int)((long)(wave + 1) * U / NW);
+  uint8_t* ldsb = lds;                                           // B operand
+  f32x4* slots = (f32x4*)(lds + (size_t)p.KQ * kSteps * 64 * 32);  // [NW][maxseg][SLOT]
+  const size_t blk_base = (size_t)(g * p.G) * p.C + (size_t)q * p.KQ;
+  const uint32_t lw = (uint32_t)lane * 16u, le = 4096u + (uint32_t)lane * 4u;
+
+  // A wave without units still issues its prologue loads (of a valid unit) so that every load
+  // before the staging barrier is unconditional.
+  const int u0 = ua < ub ? ua : 0;
+  GPos cur;
+  cur.unit = u0;
+  cur.part = 0;
+  cur.tl = u0 / p.KQ;
+  cur.s = u0 - cur.tl * p.KQ;
+  // Three register stages: while stage i is dequantised and multiplied the loads of stages i+1
+  // and i+2 are in flight, and stage i+3 is issued right after stage i is consumed.  The first
+  // three stages are issued before the B staging so that HBM streams while the activations
+  // arrive.  The steady-state loop only issues unconditional loads (a predicated load would make
+  // the compiler wait for every outstanding load); the last <= 5 stages are peeled.
+  GStage<WF, NMAT, SPS> s0, s1, s2;
+  const int nst = (ub - ua) * SPU;
+  GPos P0 = cur, P1 = cur, P2 = cur;
+  if (nst > 1) gadvance<SPU>(P1, p.KQ);
+  P2 = P1;
+  if (nst > 2) gadvance<SPU>(P2, p.KQ);
+  BStage<NW, MAXCH> bs;
+  stage_b_issue<NW, MAXCH>(p, q * p.KQ * kSuperK, bs);
+  gload(s0, p, blk_base, P0, lw, le);
+  gload(s1, p, blk_base, P1, lw, le);  // repeats stage 0 when nst == 1
+  gload(s2, p, blk_base, P2, lw, le);
+  stage_b_finish<NW, MAXCH>(p, bs, ldsb, s_t, s_ss);
+  __syncthreads();
+
+  if (ua < ub) {
+    f32x4 acc[NMAT][2];
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) acc[mat][0] = acc[mat][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int tile0 = cur.tl;
+    auto park = [&](int tl) {
+      f32x4* slot = slots + (size_t)(wave * p.maxseg + (tl - tile0)) * SLOT;
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat) {
+        slot[mat * 64 + lane] = acc[mat][0] + acc[mat][1];
+        acc[mat][0] = acc[mat][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    int i = 0;
+    for (; i + 5 < nst; i += 3) {
+      gcompute(s0, P0, ldsb, lane, acc);
+      GPos P3 = P2;
+      gadvance<SPU>(P3, p.KQ);
+      gload(s0, p, blk_base, P3, lw, le);
+      if (P1.tl != P0.tl) park(P0.tl);
+      gcompute(s1, P1, ldsb, lane, acc);
+      GPos P4 = P3;
+      gadvance<SPU>(P4, p.KQ);
+      gload(s1, p, blk_base, P4, lw, le);
+      if (P2.tl != P1.tl) park(P1.tl);
+      gcompute(s2, P2, ldsb, lane, acc);
+      GPos P5 = P4;
+      gadvance<SPU>(P5, p.KQ);
+      gload(s2, p, blk_base, P5, lw, le);
+      if (P3.tl != P2.tl) park(P2.tl);
+      P0 = P3;
+      P1 = P4;
+      P2 = P5;
+    }
+    // tail: r = 1..5 stages left; P0..P2 (those that exist) are loaded, P3, P4 are not
+    const int r = nst - i;
+    GPos last = P0, P3 = P2, P4 = P2;
+    gcompute(s0, P0, ldsb, lane, acc);
+    if (r > 3) {
+      gadvance<SPU>(P3, p.KQ);
+      gload(s0, p, blk_base, P3, lw, le);
+    }
+    if (r > 1) {
+      if (P1.tl != P0.tl) park(P0.tl);
+      gcompute(s1, P1, ldsb, lane, acc);
+      last = P1;
+      if (r > 4) {
+        P4 = P3;
+        gadvance<SPU>(P4, p.KQ);
+        gload(s1, p, blk_base, P4, lw, le);
+      }
+      if (r > 2) {
+        if (P2.tl != P1.tl) park(P1.tl);
+        gcompute(s2, P2, ldsb, lane, acc);
+        last = P2;
+        if (r > 3) {
+          if (P3.tl != P2.tl) park(P2.tl);
+          gcompute(s0, P3, ldsb, lane, acc);
+          last = P3;
+          if (r > 4) {
+            if (P4.tl != P3.tl) park(P3.tl);
+            gcompute(s1, P4, ldsb, lane, acc);
+            last = P4;
+          }
+        }
+      }
+    }
+    park(last.tl);
+  }
+  __syncthreads();
+
+  // publish this workgroup's per-tile partial sums
+  const int m = lane & 15;
+  for (int tl = wave; tl < Gw; tl += NW) {
+    f32x4 sum[NMAT];
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) sum[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int v = 0; v < NW; ++v) {
+      const int va = (int)((long)v * U / NW), vb = (int)((long)(v + 1) * U / NW);
+      if (va >= vb) continue;
+      const int vt0 = va / p.KQ, vt1 = (vb - 1) / p.KQ;
+      if (tl < vt0 || tl > vt1) continue;
+      const f32x4* slot = slots + (size_t)(v * p.maxseg + (tl - vt0)) * SLOT;
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat) sum[mat] += slot[mat * 64 + lane];
+    }
+    if (p.x_scale) {
+      const int t = s_t[m];
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sum[mat][v] = __builtin_amdgcn_ldexpf(sum[mat][v], -t);
+    }
+    float* dst = p.part + (((size_t)w * p.G + tl) * SLOT) * 4;
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) store_agent(dst + (mat * 64 + lane) * 4, sum[mat]);
+  }
+  if (p.x_scale && threadIdx.x < 16)
+    __hip_atomic_store(p.pss + (size_t)w * 16 + threadIdx.x, s_ss[threadIdx.x], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();  // every thread's stores have completed (workgroup-scope release)
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(p.counters + g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = old == p.S - 1;
+    if (last) __hip_atomic_store(p.counters + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // last arrival: sum the S partials of every tile in K order and run the epilogue
+  int th = 0;
+  if (p.x_scale) {
+    float ss = 0.f;
+    for (int qq = 0; qq < p.S; ++qq)
+      ss += __hip_atomic_load(p.pss + (size_t)(g * p.S + qq) * 16 + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const double gn = __longlong_as_double((long long)p.tg->max_row_norm_bits);
+    const double un = __longlong_as_double((long long)p.tu->max_row_norm_bits);
+    const double bound = (double)ss * gn * un * (1.0 + 1.0 / 64.0);
+    int eb = 0;
+    if (bound > 0.0) frexp(bound, &eb);
+    th = bound > 0.0 ? 15 - eb : 0;
+    if (g == 0 && threadIdx.x < 16) p.th_out[threadIdx.x] = th;
+  }
+  for (int tl = wave; tl < Gw; tl += NW) {
+    f32x4 tot[NMAT];
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat) tot[mat] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // all S slots are loaded before the (ordered) sum
+    constexpr int QB = 4;
+    for (int q0 = 0; q0 < p.S; q0 += QB) {
+      f32x4 v[QB][NMAT];
+#pragma unroll
+      for (int qq = 0; qq < QB; ++qq)
+        if (q0 + qq < p.S) {
+          const float* src = p.part + (((size_t)(g * p.S + q0 + qq) * p.G + tl) * SLOT) * 4;
+#pragma unroll
+          for (int mat = 0; mat < NMAT; ++mat) v[qq][mat] = load_agent(src + (mat * 64 + lane) * 4);
+        }
+#pragma unroll
+      for (int qq = 0; qq < QB; ++qq)
+        if (q0 + qq < p.S)
+#pragma unroll
+          for (int mat = 0; mat < NMAT; ++mat) tot[mat] += v[qq][mat];
+    }
+    gepilogue<WF, NMAT>(p, g * p.G + tl, tot, lane, th);
+  }
+}
+
+// ---------------------------------------------------------------- host side
+
+constexpr int kGemvNW = 8;
+constexpr int kGemvMaxChunks = 17;  // B staging chunks per thread (= superblocks per K split)
+constexpr int kGemvMaxLds = 160 * 1024 - 1024;  // dynamic LDS; the rest holds the static arrays
+
+static size_t gemv_lds_bytes(const GemvPlan& pl, int nmat) {
+  return (size_t)pl.KQ * kSteps * 64 * 32 + (size_t)kGemvNW * pl.maxseg * nmat * 64 * 16;
+}
+
+// Work split: minimise a simple time model over the K split S.  A workgroup streams U = G * KQ
+// units (NMAT x 4352-byte blocks each); the last workgroup of a tile group then reads S * G
+// partial tiles (NMAT KB each).  Units cost ~0.16 us per matrix at a CU's share of HBM
+// bandwidth, partial tiles ~0.05 us per KB (measured on MI355X); splits using fewer than all
+// CUs pay for it through their larger U.
+int plan_gemv(int rows, int K, int nmat, int num_cus, GemvPlan* out) {
+  if (rows <= 0 || K <= 0 || rows % kTileRows || K % kSuperK) return -1;
+  const int T = rows / kTileRows, C = K / kSuperK;
+  const int cus = num_cus < 1 ? 1 : (num_cus > kMaxWorkgroups ? kMaxWorkgroups : num_cus);
+  GemvPlan best{};
+  double best_cost = -1.0;
+  for (int S = 1; S <= C && S <= kMaxSplit; ++S) {
+    if (C % S) continue;
+    const int KQ = C / S;
+    if (KQ > kGemvMaxChunks) continue;  // B staging registers
+    const int G = (int)(((long)T * S + cus - 1) / cus);
+    const int Ng = (T + G - 1) / G;
+    const int P = Ng * S;
+    if (P > cus) continue;
+    const int U = G * KQ;
+    const int per = (U + kGemvNW - 1) / kGemvNW;
+    GemvPlan c{G, S, KQ, Ng, P, (per - 1 + KQ - 1) / KQ + 1};
+    if (gemv_lds_bytes(c, nmat) > (size_t)kGemvMaxLds) continue;
+    const double cost = U * 0.16 * nmat + (S > 1 ? S * G * nmat * 0.05 : 0.0);
+    if (best_cost < 0 || cost < best_cost - 1e-9) {
+      best = c;
+      best_cost = cost;
+    }
+  }
+  if (best_cost < 0) return -2;
+  *out = best;
+  return 0;
+}
+
+template <int WF, int NMAT, int MAXCH>
+static int launch_gemv_ch(const GvParams& p, size_t lds, hipStream_t s) {
+  auto kern = gemv_kernel<WF, NMAT, kGemvNW, MAXCH>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLds) != hipSuccess)
+      return set_error(-4, "gemv_kernel: cannot enable 160 KB LDS");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(p.P), dim3(kGemvNW * 64), lds, s, p);
+  return check_launch("gemv_kernel");
+}
+
+// The staging register array is sized by a small set of buckets (loads beyond KQ are clamped
+// duplicates).
+template <int WF, int NMAT>
+static int launch_gemv(const GvParams& p, size_t lds, hipStream_t s) {
+  if (p.KQ <= 4) return launch_gemv_ch<WF, NMAT, 4>(p, lds, s);
+  if (p.KQ <= 10) return launch_gemv_ch<WF, NMAT, 10>(p, lds, s);
+  return launch_gemv_ch<WF, NMAT, kGemvMaxChunks>(p, lds, s);
+}
+
+size_t gemv_max_slots(int rows, int K, int nmat) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, int>, size_t> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(rows, K, nmat);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  size_t best = 0;
+  for (int cus = 1; cus <= kMaxWorkgroups; ++cus) {
+    GemvPlan pl;
+    if (plan_gemv(rows, K, nmat, cus, &pl) == 0) best = std::max(best, (size_t)pl.P * pl.G);
+  }
+  cache[key] = best;
+  return best;
+}
+
+bool gemv_supported(int M, int H, int I, int num_cus) {
+  GemvPlan a, b;
+  return M >= 1 && M <= 16 && plan_gemv(I, H, 2, num_cus, &a) == 0 && plan_gemv(H, I, 1, num_cus, &b) == 0;
+}
+
+int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s) {
+  const WsLayout L = ws_layout(a.M, a.H, a.I, a.fmt);
+  const int fmt = a.fmt;
+  GemvPlan pg, pd;
+  if (plan_gemv(a.I, a.H, 2, num_cus, &pg) || plan_gemv(a.H, a.I, 1, num_cus, &pd))
+    return set_error(-1, "no weight-streaming split for H=%d I=%d", a.H, a.I);
+  int* th = (int*)(a.ws + L.th);
+  uint16_t* h = (uint16_t*)(a.ws + L.h);
+  profile_mark(0, s);
+  profile_mark(1, s);
+  GvParams g{};
+  g.w0 = a.wg;
+  g.w1 = a.wu;
+  g.rowexp0 = (const int*)(a.wg + rowexp_offset(a.I, a.H, fmt));
+  g.rowexp1 = (const int*)(a.wu + rowexp_offset(a.I, a.H, fmt));
+  g.src = (const uint16_t*)a.x;
+  g.M = a.M;
+  g.K = a.H;
+  g.N = a.I;
+  g.C = a.H / kSuperK;
+  g.T = a.I / kTileRows;
+  g.G = pg.G;
+  g.S = pg.S;
+  g.KQ = pg.KQ;
+  g.Ng = pg.Ng;
+  g.P = pg.P;
+  g.maxseg = pg.maxseg;
+  g.x_scale = fmt == 1;
+  g.th_out = th;
+  g.tg = (const Trailer*)(a.wg + trailer_offset(a.I, a.H, fmt));
+  g.tu = (const Trailer*)(a.wu + trailer_offset(a.I, a.H, fmt));
+  g.out = h;
+  g.part = (float*)(a.ws + L.part_gu);
+  g.pss = (float*)(a.ws + L.pss);
+  g.counters = (int*)(a.ws + L.counters_gu);
+  int rc = fmt == 1 ? launch_gemv<1, 2>(g, gemv_lds_bytes(pg, 2), s) : launch_gemv<0, 2>(g, gemv_lds_bytes(pg, 2), s);
+  if (rc) return rc;
+  profile_mark(2, s);
+  GvParams d{};
+  d.w0 = a.wd;
+  d.rowexp0 = (const int*)(a.wd + rowexp_offset(a.H, a.I, fmt));
+  d.src = h;
+  d.M = a.M;
+  d.K = a.I;
+  d.N = a.H;
+  d.C = a.I / kSuperK;
+  d.T = a.H / kTileRows;
+  d.G = pd.G;
+  d.S = pd.S;
+  d.KQ = pd.KQ;
+  d.Ng = pd.Ng;
+  d.P = pd.P;
+  d.maxseg = pd.maxseg;
+  d.x_scale = 0;
+  d.th_in = th;
+  d.out = a.out;
+  d.residual = a.residual;
+  d.out_f32 = a.out_f32;
+  d.res_f32 = a.res_f32;
+  d.part = (float*)(a.ws + L.part_d);
+  d.counters = (int*)(a.ws + L.counters_d);
+  rc = fmt == 1 ? launch_gemv<1, 1>(d, gemv_lds_bytes(pd, 1), s) : launch_gemv<0, 1>(d, gemv_lds_bytes(pd, 1), s);
+  if (rc) return rc;
+  profile_mark(3, s);
+  return 0;
+}
+
+}  // namespace qmlp

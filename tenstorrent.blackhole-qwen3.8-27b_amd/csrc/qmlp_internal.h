@@ -10,6 +10,10 @@ namespace qmlp {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// Optional per-kernel events of the forward pass (qmlp_set_profile_events).
+void set_profile_events(const hipEvent_t* ev);
+void profile_mark(int i, hipStream_t s);
+
 // Load-time kernels (qmlp_pack.hip).
 int launch_quantize(const void* w, int rows, int cols, void* q, void* e8, uint32_t* bad, hipStream_t s);
 int launch_pack(const void* src0, const void* src1, int rows, int cols, int fmt, void* packed, hipStream_t s);
@@ -29,6 +33,21 @@ constexpr int kMaxWorkgroups = 512;  // upper bound used to size the workspace
 constexpr int kMaxSeg = 2;            // tiles one wave may touch
 int plan_skinny(int rows, int K, int M, int num_cus, SkinnyPlan* plan);
 
+// 2-D split of one projection for the M <= 16 weight-streaming kernel (qmlp_gemv.hip).
+struct GemvPlan {
+  int G;       // tiles per group
+  int S;       // K splits
+  int KQ;      // superblocks per K split
+  int Ng;      // tile groups
+  int P;       // workgroups = Ng * S
+  int maxseg;  // tiles one wave may touch
+};
+constexpr int kMaxSplit = 16;
+int plan_gemv(int rows, int K, int nmat, int num_cus, GemvPlan* out);
+bool gemv_supported(int M, int H, int I, int num_cus);
+// Largest partial-slot count (P * G) any device could need for this projection (workspace size).
+size_t gemv_max_slots(int rows, int K, int nmat);
+
 // Workspace layout for one forward call.
 struct WsLayout {
   size_t counters_gu, counters_d;  // int32 per tile
@@ -36,6 +55,7 @@ struct WsLayout {
   size_t x16;                      // f16 [M, H] (bfp8 only)
   size_t h;                        // 16-bit [M, I]
   size_t part_gu, part_d;          // fp32 partial-sum slots
+  size_t pss;                      // per-workgroup token sums of squares (bfp8)
   size_t total;
 };
 WsLayout ws_layout(int M, int H, int I, int fmt);
@@ -54,5 +74,6 @@ struct ForwardArgs {
 };
 int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s);
 int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s);
+int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s);
 
 }  // namespace qmlp

@@ -9,9 +9,9 @@
 //            |h| <= |x_m|^2 max|Wg_n| max|Wu_n| so that h * 2^th[m] fits fp16.
 //   gate/up  one kernel streams Wg and Wu tile by tile; per 16-row tile the products of both
 //            matrices accumulate in fp32 matrix-core registers; the epilogue applies the row and
-//            token scales, h = bf16(silu(g) * u) (one rounding, as the reference's fused
-//            epilogue), and writes h (bf16, or fp16 * 2^th for bfp8).  Gate and up never leave
-//            registers.
+//            token scales, h = silu(g) * u rounded once -- to bf16 for the bf16-weight kernels (as
+//            the reference's fused epilogue), to fp16 * 2^th for bfp8 -- and writes h.  Gate and up
+//            never leave registers.
 //   down     same kernel with one matrix over K = I; epilogue out = residual + y, written as bf16
 //            (rounded once) or fp32.
 //
@@ -86,42 +86,54 @@ __device__ __forceinline__ void advance(Pos& q, int C) {
   }
 }
 
+// Per-lane byte offsets, computed once: weights (lane * 16), exponents (lane * 4) and the B
+// operand row of each column tile.  Token rows beyond M read row M-1 instead: column m of the B
+// operand only feeds output column m, which the epilogue never stores, and unconditional loads
+// keep the compiler's wait counts exact (a predicated load forces a wait for every load).
+template <int NCT>
+struct LaneOffsets {
+  uint32_t w, e, b[NCT];
+};
+
+template <int NCT>
+__device__ __forceinline__ LaneOffsets<NCT> lane_offsets(const SkParams& p, int lane) {
+  LaneOffsets<NCT> o;
+  o.w = (uint32_t)lane * 16u;
+  o.e = 4096u + (uint32_t)lane * 4u;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ++ct) {
+    const int m = min(ct * 16 + (lane & 15), p.M - 1);
+    o.b[ct] = ((uint32_t)m * (uint32_t)p.K + (uint32_t)(lane >> 4) * 16u) * 2u;
+  }
+  return o;
+}
+
 template <int WF, int NMAT, int NCT, int SPS>
 __device__ __forceinline__ void load_stage(Stage<WF, NMAT, NCT, SPS>& s, const SkParams& p, const Pos& q,
-                                           int lane) {
+                                           const LaneOffsets<NCT>& o) {
   constexpr int BLK = WF ? kBfp8Block : kBf16Block;
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
-    const uint8_t* blk = (mat ? p.w1 : p.w0) + (size_t)q.unit * BLK;
+    const uint8_t* blk = (mat ? p.w1 : p.w0) + (size_t)q.unit * BLK + q.part * SPS * (WF ? 1024 : 2048);
 #pragma unroll
     for (int jj = 0; jj < SPS; ++jj) {
-      const int j = q.part * SPS + jj;
       if constexpr (WF) {
-        s.w[mat][jj][0] = ld_stream((const u32x4*)(blk + j * 1024 + lane * 16));
+        s.w[mat][jj][0] = ld_stream((const u32x4*)(blk + o.w + jj * 1024));
       } else {
-        s.w[mat][jj][0] = ld_stream((const u32x4*)(blk + j * 2048 + lane * 16));
-        s.w[mat][jj][1] = ld_stream((const u32x4*)(blk + j * 2048 + 1024 + lane * 16));
+        s.w[mat][jj][0] = ld_stream((const u32x4*)(blk + o.w + jj * 2048));
+        s.w[mat][jj][1] = ld_stream((const u32x4*)(blk + o.w + jj * 2048 + 1024));
       }
     }
-    if constexpr (WF) s.e[mat] = ld_stream((const uint32_t*)(blk + 4096 + lane * 4));
+    if constexpr (WF) s.e[mat] = ld_stream((const uint32_t*)((mat ? p.w1 : p.w0) + (size_t)q.unit * BLK + o.e));
   }
-  const int quarter = lane >> 4;
+  const uint8_t* bk = (const uint8_t*)p.B + (size_t)(q.c * kSuperK + q.part * SPS * 64) * 2;
 #pragma unroll
-  for (int ct = 0; ct < NCT; ++ct) {
-    const int m = ct * 16 + (lane & 15);
+  for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
     for (int jj = 0; jj < SPS; ++jj) {
-      const int j = q.part * SPS + jj;
-      if (m < p.M) {
-        const uint16_t* bp = p.B + (size_t)m * p.K + q.c * kSuperK + j * 64 + quarter * 16;
-        s.b[ct][jj][0] = *(const u32x4*)bp;
-        s.b[ct][jj][1] = *(const u32x4*)(bp + 8);
-      } else {
-        s.b[ct][jj][0] = u32x4{0u, 0u, 0u, 0u};
-        s.b[ct][jj][1] = u32x4{0u, 0u, 0u, 0u};
-      }
+      s.b[ct][jj][0] = *(const u32x4*)(bk + o.b[ct] + jj * 128);
+      s.b[ct][jj][1] = *(const u32x4*)(bk + o.b[ct] + jj * 128 + 16);
     }
-  }
 }
 
 template <int WF, int NMAT, int NCT, int SPS>
@@ -175,8 +187,10 @@ __device__ __forceinline__ void epilogue(const SkParams& p, int t, const f32x4 (
           u = __builtin_amdgcn_ldexpf(u, p.rowexp1[nb + v] - p.bscale[m]);
         }
         const float hv = g / (1.0f + expf(-g)) * u;
-        const uint16_t hb = f32_to_bf16(hv);
-        o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(bf16_to_f32(hb), p.hscale[m])) : hb;
+        // bf16 weights: h is the bf16 matrix-core operand of the down projection, rounded once like
+        // the reference's fused epilogue.  bfp8: h is kept as an fp16 operand (11 significant
+        // bits) scaled by 2^hscale, one rounding from fp32.
+        o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(hv, p.hscale[m])) : f32_to_bf16(hv);
       }
     } else {
       float y[4];
@@ -271,8 +285,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkParams p) {
   int a, b;
   wg_range(p, w, a, b);
   const int spt = SPU * p.C;  // stages per tile
-  const int sa = a * SPU + (int)((long)wave * (b - a) * SPU / NW);
-  const int sb = a * SPU + (int)((long)(wave + 1) * (b - a) * SPU / NW);
+  const int sa = __builtin_amdgcn_readfirstlane(a * SPU + (int)((long)wave * (b - a) * SPU / NW));
+  const int sb = __builtin_amdgcn_readfirstlane(a * SPU + (int)((long)(wave + 1) * (b - a) * SPU / NW));
 
   if (sa < sb) {
     f32x4 acc[NMAT][NCT][2];
@@ -292,34 +306,42 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkParams p) {
           acc[mat][ct][0] = acc[mat][ct][1] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     };
-    Pos ld;
-    ld.st = sa;
-    ld.unit = sa / SPU;
-    ld.part = sa % SPU;
-    ld.c = ld.unit % p.C;
+    // Ping-pong over two register stages: the loads of stage st+1 are in flight while stage st
+    // is dequantised and multiplied.  Past the end of the range the prefetch repeats the last
+    // stage (never computed) so that every load is unconditional.
+    const LaneOffsets<NCT> lo = lane_offsets<NCT>(p, lane);
+    Pos cur;
+    cur.st = sa;
+    cur.unit = sa / SPU;
+    cur.part = sa % SPU;
+    cur.c = __builtin_amdgcn_readfirstlane(cur.unit % p.C);
     Stage<WF, NMAT, NCT, SPS> s0, s1;
-    load_stage(s0, p, ld, lane);
-    int part0 = ld.part;
-    for (int st = sa; st < sb; st += 2) {
-      advance<SPU>(ld, p.C);
-      int part1 = ld.part;
-      if (st + 1 < sb) load_stage(s1, p, ld, lane);
+    load_stage(s0, p, cur, lo);
+    const int pairs = (sb - sa + 1) >> 1;
+    for (int it = 0; it < pairs; ++it) {
+      const int st = sa + 2 * it;
+      Pos n1 = cur;
+      advance<SPU>(n1, p.C);
+      if (st + 1 >= sb) n1 = cur;
+      load_stage(s1, p, n1, lo);
       if (st >= boundary) {
         park();
         ++seg;
         boundary += spt;
       }
-      compute_stage(s0, part0, acc);
+      compute_stage(s0, cur.part, acc);
       if (st + 1 >= sb) break;
-      advance<SPU>(ld, p.C);
-      part0 = ld.part;
-      if (st + 2 < sb) load_stage(s0, p, ld, lane);
+      Pos n2 = n1;
+      advance<SPU>(n2, p.C);
+      if (st + 2 >= sb) n2 = n1;
+      load_stage(s0, p, n2, lo);
       if (st + 1 >= boundary) {
         park();
         ++seg;
         boundary += spt;
       }
-      compute_stage(s1, part1, acc);
+      compute_stage(s1, n1.part, acc);
+      cur = n2;
     }
     park();
   }
@@ -448,6 +470,7 @@ int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s) {
   int* th = (int*)(a.ws + L.th);
   uint16_t* x16 = (uint16_t*)(a.ws + L.x16);
   uint16_t* h = (uint16_t*)(a.ws + L.h);
+  profile_mark(0, s);
   if (fmt == 1) {
     const Trailer* tg = (const Trailer*)(a.wg + trailer_offset(a.I, a.H, 1));
     const Trailer* tu = (const Trailer*)(a.wu + trailer_offset(a.I, a.H, 1));
@@ -455,6 +478,7 @@ int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s) {
     int rc = check_launch("prep_kernel");
     if (rc) return rc;
   }
+  profile_mark(1, s);
   SkinnyPlan pg, pd;
   if (plan_skinny(a.I, a.H, 32, num_cus, &pg) || plan_skinny(a.H, a.I, 32, num_cus, &pd))
     return set_error(-1, "bad projection shape H=%d I=%d", a.H, a.I);
@@ -484,6 +508,7 @@ int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s) {
     g.counters = (int*)(a.ws + L.counters_gu);
     int rc = fmt == 1 ? launch_proj_m<1, 2>(g, s) : launch_proj_m<0, 2>(g, s);
     if (rc) return rc;
+    if (m0 + 32 >= a.M) profile_mark(2, s);
     SkParams d{};
     d.w0 = a.wd;
     d.w1 = nullptr;
@@ -508,6 +533,7 @@ int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s) {
     rc = fmt == 1 ? launch_proj_m<1, 1>(d, s) : launch_proj_m<0, 1>(d, s);
     if (rc) return rc;
   }
+  profile_mark(3, s);
   return 0;
 }
 
