@@ -75,6 +75,9 @@ __device__ __forceinline__ T ld_stream(const T* p) {  // streamed once: do not k
   return __builtin_nontemporal_load(p);
 }
 
+// s_waitcnt operand: vector memory counter 0, export and LDS/scalar counters not waited on.
+constexpr int kWaitVmcnt0 = 0x0f70;
+
 // ---------------------------------------------------------------- bfp8 in-register dequant
 //
 // Mantissa byte u (excess-128) and the byte-permute constant 0x64 form the half 0x64uu = 1024+u.

@@ -19,7 +19,7 @@
 //      stream their weight blocks (ping-pong register stages, non-temporal 16-byte loads),
 //      dequantising in registers; partial sums are parked in LDS at tile boundaries;
 //   3. after one barrier each tile's partials are summed in wave order and published to a
-//      workspace slot; one release fence + one arrival counter per workgroup;
+//      workspace slot; each thread waits for its stores, then one arrival counter per workgroup;
 //   4. the last of the S workgroups of a tile group sums the S slots in K order (deterministic)
 //      and runs the epilogue: gate/up -> h = silu(g) * u (bf16, or fp16 * 2^th for bfp8),
 //      down -> out = residual + y (bf16 or fp32).  It resets the counter for the next call.
@@ -146,19 +146,26 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, const BStage<N
   }
 }
 
-// Partial sums cross workgroups (and XCDs) through agent-scope relaxed atomic stores and loads:
-// they are coherent at the device level by themselves, so publishing needs no L2 write-back and
-// reading no L2 invalidation -- only the wait for the stores before the arrival counter moves.
-__device__ __forceinline__ void store_agent(float* p, f32x4 v) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) __hip_atomic_store(p + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Partial sums cross workgroups (and XCDs) through device-coherent 16-byte buffer stores and loads
+// (the sc1 cache policy of agent-scope atomic accesses, on whole 16-byte lanes so that one
+// instruction writes or reads whole lines): coherent at the device level by themselves, so
+// publishing needs no L2 write-back and reading no L2 invalidation -- only the wait for the stores
+// before the arrival counter moves.  The descriptor's extent bounds every access.
+constexpr int kCoherent = 16;                   // buffer cache-policy operand: sc1
+constexpr int kBufferRsrcWord3 = 0x00020000;    // raw (untyped) buffer descriptor, gfx9
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const GvParams& p, int nmat) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p.part, 0, p.P * p.G * nmat * 64 * 16, kBufferRsrcWord3);
 }
-__device__ __forceinline__ f32x4 load_agent(const float* p) {
-  f32x4 v;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return v;
+__device__ __forceinline__ void store_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kCoherent);
 }
+__device__ __forceinline__ f32x4 load_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherent));
+}
+// Waits until this thread's global loads and stores have completed.  A workgroup barrier does not
+// wait for global stores, so every thread calls this before the barrier that precedes an arrival
+// counter: the counter then moves only after the stores it announces are visible device-wide.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); }
 
 // ---------------------------------------------------------------- main loop pieces
 
@@ -403,6 +410,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 
   // publish this workgroup's per-tile partial sums
   const int m = lane & 15;
+  const __amdgpu_buffer_rsrc_t prs = part_rsrc(p, NMAT);
   for (int tl = wave; tl < Gw; tl += NW) {
     f32x4 sum[NMAT];
 #pragma unroll
@@ -423,14 +431,15 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) sum[mat][v] = __builtin_amdgcn_ldexpf(sum[mat][v], -t);
     }
-    float* dst = p.part + (((size_t)w * p.G + tl) * SLOT) * 4;
+    const uint32_t dst = (uint32_t)((w * p.G + tl) * SLOT + lane) * 16u;
 #pragma unroll
-    for (int mat = 0; mat < NMAT; ++mat) store_agent(dst + (mat * 64 + lane) * 4, sum[mat]);
+    for (int mat = 0; mat < NMAT; ++mat) store_coherent(prs, dst + mat * 1024u, sum[mat]);
   }
   if (p.x_scale && threadIdx.x < 16)
     __hip_atomic_store(p.pss + (size_t)w * 16 + threadIdx.x, s_ss[threadIdx.x], __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();  // every thread's stores have completed (workgroup-scope release)
+  wait_stores();
+  __syncthreads();
   if (threadIdx.x == 0) {
     const int old = __hip_atomic_fetch_add(p.counters + g, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int last = old == p.S - 1;
@@ -465,9 +474,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
       for (int qq = 0; qq < QB; ++qq)
         if (q0 + qq < p.S) {
-          const float* src = p.part + (((size_t)(g * p.S + q0 + qq) * p.G + tl) * SLOT) * 4;
+          const uint32_t src = (uint32_t)(((g * p.S + q0 + qq) * p.G + tl) * SLOT + lane) * 16u;
 #pragma unroll
-          for (int mat = 0; mat < NMAT; ++mat) v[qq][mat] = load_agent(src + (mat * 64 + lane) * 4);
+          for (int mat = 0; mat < NMAT; ++mat) v[qq][mat] = load_coherent(prs, src + mat * 1024u);
         }
 #pragma unroll
       for (int qq = 0; qq < QB; ++qq)
