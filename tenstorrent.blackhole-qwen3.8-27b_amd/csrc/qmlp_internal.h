@@ -72,8 +72,11 @@ struct ForwardArgs {
   int M, H, I, fmt;
   int out_f32, res_f32;  // fp32 output / fp32 residual instead of bf16
 };
+// bfp8: x -> x16 = fp16(x * 2^tx[m]) and the h scale th[m], for all M tokens (qmlp_skinny.hip).
+int launch_prep(const ForwardArgs& a, hipStream_t s);
 int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s);
 int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s);
+bool tiled_supported(int M, int H, int I);
 int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s);
 
 }  // namespace qmlp

@@ -463,6 +463,15 @@ static int launch_proj_m(const SkParams& p, hipStream_t s) {
   return p.M <= 16 ? launch_proj<WF, NMAT, 1>(p, s) : launch_proj<WF, NMAT, 2>(p, s);
 }
 
+int launch_prep(const ForwardArgs& a, hipStream_t s) {
+  const WsLayout L = ws_layout(a.M, a.H, a.I, a.fmt);
+  const Trailer* tg = (const Trailer*)(a.wg + trailer_offset(a.I, a.H, 1));
+  const Trailer* tu = (const Trailer*)(a.wu + trailer_offset(a.I, a.H, 1));
+  hipLaunchKernelGGL(prep_kernel, dim3(a.M), dim3(256), 0, s, (const uint16_t*)a.x, a.H, tg, tu,
+                     (uint16_t*)(a.ws + L.x16), (int*)(a.ws + L.tx), (int*)(a.ws + L.th));
+  return check_launch("prep_kernel");
+}
+
 int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s) {
   const WsLayout L = ws_layout(a.M, a.H, a.I, a.fmt);
   const int fmt = a.fmt;
@@ -472,10 +481,7 @@ int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s) {
   uint16_t* h = (uint16_t*)(a.ws + L.h);
   profile_mark(0, s);
   if (fmt == 1) {
-    const Trailer* tg = (const Trailer*)(a.wg + trailer_offset(a.I, a.H, 1));
-    const Trailer* tu = (const Trailer*)(a.wu + trailer_offset(a.I, a.H, 1));
-    hipLaunchKernelGGL(prep_kernel, dim3(a.M), dim3(256), 0, s, (const uint16_t*)a.x, a.H, tg, tu, x16, tx, th);
-    int rc = check_launch("prep_kernel");
+    int rc = launch_prep(a, s);
     if (rc) return rc;
   }
   profile_mark(1, s);

@@ -1,0 +1,330 @@
+// qmlp_tiled.hip -- matrix-core GEMM kernels for many tokens (prefill chunks).
+//
+// Reference realisation being replaced: the prefill branch of Qwen36MLP -- the fused gate/up
+// with SiLU on fp32 accumulators (docker/qwen-c2-graft/graft/mlp.py:440-456, rounded once,
+// docs/real-text-2026-09-24.md:272-276) and the down projection with its prefill program config
+// (mlp.py:539-611).
+//
+// Formulation: out^T[n, m] = sum_k W[n, k] x[m, k].  The weights are the matrix-core A operand:
+// each wave owns TPW 16-row tiles of each matrix and streams them through registers in the packed
+// layout (bfp8 dequantised exactly to fp16 in registers, bf16 used as is).  The tokens are the
+// B operand: a block stages MG groups of 16 token rows, one 64-K step at a time, into a 3-slot LDS
+// ring shared by all its waves (the same lane order as the weight-streaming kernels, so each lane
+// reads its B fragment with two 16-byte LDS loads).  One block = NWV waves x TPW tiles x NMAT
+// matrices of features by MG x 16 tokens; every A fragment feeds MG x 2 products and every B
+// fragment NMAT x TPW x 2.
+//
+// Pipeline per 64-K step s: issue the B loads of step s+3 and compute step s from LDS slot s%3
+// and register stage s%3; issue the weight loads of step s+3 into that stage; write the B rows of
+// step s+2 (loaded one step earlier) into slot (s+2)%3; one barrier.  Loads beyond the last step
+// are clamped duplicates, so every load is unconditional.
+//
+// Epilogue (fp32 accumulators in registers): gate/up -> h = silu(g) * u rounded once (fp16 *
+// 2^th for bfp8, bf16 for bf16 weights); down -> out = residual + y.  No cross-workgroup
+// reduction: every output element is owned by one lane of one wave.
+#include "qmlp_common.h"
+#include "qmlp_internal.h"
+
+namespace qmlp {
+
+struct TlParams {
+  const uint8_t* w0;
+  const uint8_t* w1;
+  const int* rowexp0;
+  const int* rowexp1;
+  const uint16_t* src;   // [M, K] B rows: fp16 * 2^tsrc[m] (bfp8 weights) or bf16
+  int M, K, N, C;        // N output features, C = K / 256
+  int nbm;               // token blocks
+  const int* tsrc;       // bfp8: per-token exponent of src
+  const int* tout;       // bfp8 gate/up: h16 = h * 2^tout[m]
+  void* out;             // gate/up: h [M, N] 16-bit; down: out [M, N] bf16 or fp32
+  const void* residual;  // down: [M, N] bf16 or fp32, may alias out
+  int out_f32, res_f32;
+};
+
+template <int WF, int NMAT, int TPW>
+struct TlStage {
+  u32x4 w[NMAT][TPW][WF ? 1 : 2];
+  uint32_t e[NMAT][TPW];
+};
+
+template <int WF, int NMAT, int TPW, int MG, int NWV>
+__global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
+  constexpr int NT = NWV * 64;
+  constexpr int SLOT = MG * 2048;      // LDS bytes of one 64-K step of B
+  constexpr int CPT = MG * 128 / NT;   // 16-byte B chunks per thread per step
+  static_assert(CPT * NT == MG * 128, "B chunks must divide evenly over the threads");
+  constexpr int BLK = WF ? kBfp8Block : kBf16Block;
+  constexpr int SB = WF ? 1024 : 2048;  // bytes of one K-step inside a weight block
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int L = xcd_logical(blockIdx.x, gridDim.x);  // blocks sharing weights share an XCD
+  const int bn = L / p.nbm, bm = L % p.nbm;
+  const int m0 = bm * MG * 16;
+  const int tile0 = (bn * NWV + wave) * TPW;
+  const int nst = p.C * kSteps;
+
+  // B chunk c = threadIdx.x + i * NT: token row r = c / 8, 8 K values j = c % 8 of the step;
+  // quarter j / 2, half j % 2.  Rows beyond M repeat row M - 1 (their outputs are not stored).
+  uint32_t goff[CPT], loff[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + i * NT, r = c >> 3, j = c & 7;
+    const int mr = min(m0 + r, p.M - 1);
+    goff[i] = (uint32_t)(mr * p.K + j * 8) * 2u;
+    loff[i] = (uint32_t)((r >> 4) * 2048 + (((j >> 1) * 16 + (r & 15)) * 2 + (j & 1)) * 16);
+  }
+  const uint8_t* srcb = (const uint8_t*)p.src;
+  auto bload = [&](u32x4(&v)[CPT], int step) {
+    const uint8_t* base = srcb + (size_t)min(step, nst - 1) * 128;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) v[i] = *(const u32x4*)(base + goff[i]);
+  };
+  auto bstore = [&](const u32x4(&v)[CPT], int step) {
+    uint8_t* slot = lds + (step % 3) * SLOT;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) *(u32x4*)(slot + loff[i]) = v[i];
+  };
+
+  const uint8_t* wt[NMAT][TPW];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) wt[mat][t] = (mat ? p.w1 : p.w0) + (size_t)(tile0 + t) * p.C * BLK;
+  const uint32_t lw = (uint32_t)lane * 16u, le = 4096u + (uint32_t)lane * 4u;
+  // Weights are re-read by every token block of the same features, so they are loaded with the
+  // default cache policy (kept in L2 for the neighbouring blocks of the XCD).
+  auto wload = [&](TlStage<WF, NMAT, TPW>& st, int step) {
+    const int sc = min(step, nst - 1);
+    const uint32_t off = (uint32_t)(sc >> 2) * BLK + (uint32_t)(sc & 3) * SB;
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const uint8_t* b = wt[mat][t] + off;
+        st.w[mat][t][0] = *(const u32x4*)(b + lw);
+        if constexpr (WF) {
+          st.e[mat][t] = *(const uint32_t*)(wt[mat][t] + (uint32_t)(sc >> 2) * BLK + le);
+        } else {
+          st.w[mat][t][1] = *(const u32x4*)(b + 1024 + lw);
+        }
+      }
+  };
+
+  f32x4 acc[NMAT][TPW][MG];
+#pragma unroll
+  for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int g = 0; g < MG; ++g) acc[mat][t][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const TlStage<WF, NMAT, TPW>& st, int step) {
+    const uint8_t* slot = lds + (step % 3) * SLOT + lane * 32;
+    if constexpr (WF) {
+      f16x8 a[NMAT][TPW][2];
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) dq16(st.w[mat][t][0], scale_pair(st.e[mat][t], step & 3), a[mat][t][0], a[mat][t][1]);
+#pragma unroll
+      for (int g = 0; g < MG; ++g) {
+        const f16x8 b0 = __builtin_bit_cast(f16x8, *(const u32x4*)(slot + g * 2048));
+        const f16x8 b1 = __builtin_bit_cast(f16x8, *(const u32x4*)(slot + g * 2048 + 16));
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) {
+            acc[mat][t][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mat][t][0], b0, acc[mat][t][g], 0, 0, 0);
+            acc[mat][t][g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mat][t][1], b1, acc[mat][t][g], 0, 0, 0);
+          }
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < MG; ++g) {
+        const bf16x8 b0 = __builtin_bit_cast(bf16x8, *(const u32x4*)(slot + g * 2048));
+        const bf16x8 b1 = __builtin_bit_cast(bf16x8, *(const u32x4*)(slot + g * 2048 + 16));
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) {
+            acc[mat][t][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.w[mat][t][0]), b0,
+                                                                     acc[mat][t][g], 0, 0, 0);
+            acc[mat][t][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, st.w[mat][t][1]), b1,
+                                                                     acc[mat][t][g], 0, 0, 0);
+          }
+      }
+    }
+  };
+
+  TlStage<WF, NMAT, TPW> s0, s1, s2;
+  u32x4 bA[CPT], bB[CPT];
+  bload(bA, 0);
+  bload(bB, 1);
+  wload(s0, 0);
+  wload(s1, 1);
+  wload(s2, 2);
+  bstore(bA, 0);
+  bstore(bB, 1);
+  bload(bA, 2);
+  __syncthreads();
+  // iteration s: bnext receives step s+3 (it held step s+1, already in LDS); bwrite holds step
+  // s+2 and goes to slot (s+2) % 3, which was last read in iteration s-1.
+  auto iter = [&](TlStage<WF, NMAT, TPW>& cur, u32x4(&bnext)[CPT], u32x4(&bwrite)[CPT], int s) {
+    bload(bnext, s + 3);
+    compute(cur, s);
+    wload(cur, s + 3);
+    bstore(bwrite, s + 2);
+    __syncthreads();
+  };
+  int s = 0;
+  for (; s + 6 <= nst; s += 6) {
+    iter(s0, bB, bA, s);
+    iter(s1, bA, bB, s + 1);
+    iter(s2, bB, bA, s + 2);
+    iter(s0, bA, bB, s + 3);
+    iter(s1, bB, bA, s + 4);
+    iter(s2, bA, bB, s + 5);
+  }
+  const int r = nst - s;
+  if (r > 0) iter(s0, bB, bA, s);
+  if (r > 1) iter(s1, bA, bB, s + 1);
+  if (r > 2) iter(s2, bB, bA, s + 2);
+  if (r > 3) iter(s0, bA, bB, s + 3);
+  if (r > 4) iter(s1, bB, bA, s + 4);
+
+  // epilogue: lane l holds features 4 * (l / 16) + v of each tile for token l % 16 of each group
+  const int col = lane & 15, rq = (lane >> 4) * 4;
+#pragma unroll
+  for (int g = 0; g < MG; ++g) {
+    const int m = m0 + g * 16 + col;
+    if (m >= p.M) continue;
+    const int ts = WF ? p.tsrc[m] : 0;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int n = (tile0 + t) * kTileRows + rq;
+      uint16_t o[4];
+      if constexpr (NMAT == 2) {
+        const int to = WF ? p.tout[m] : 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float gv = acc[0][t][g][v], uv = acc[1][t][g][v];
+          if constexpr (WF) {
+            gv = __builtin_amdgcn_ldexpf(gv, p.rowexp0[n + v] - ts);
+            uv = __builtin_amdgcn_ldexpf(uv, p.rowexp1[n + v] - ts);
+          }
+          const float hv = gv / (1.0f + expf(-gv)) * uv;
+          o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(hv, to)) : f32_to_bf16(hv);
+        }
+      } else {
+        float y[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          y[v] = acc[0][t][g][v];
+          if constexpr (WF) y[v] = __builtin_amdgcn_ldexpf(y[v], p.rowexp0[n + v] - ts);
+        }
+        if (p.residual) {
+          if (p.res_f32) {
+            const f32x4 rr = *(const f32x4*)((const float*)p.residual + (size_t)m * p.N + n);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) y[v] += rr[v];
+          } else {
+            const u32x2 rr = *(const u32x2*)((const uint16_t*)p.residual + (size_t)m * p.N + n);
+            y[0] += bf16_to_f32((uint16_t)(rr.x & 0xffffu));
+            y[1] += bf16_to_f32((uint16_t)(rr.x >> 16));
+            y[2] += bf16_to_f32((uint16_t)(rr.y & 0xffffu));
+            y[3] += bf16_to_f32((uint16_t)(rr.y >> 16));
+          }
+        }
+        if (p.out_f32) {
+          *(f32x4*)((float*)p.out + (size_t)m * p.N + n) = f32x4{y[0], y[1], y[2], y[3]};
+          continue;
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(y[v]);
+      }
+      *(u32x2*)((uint16_t*)p.out + (size_t)m * p.N + n) =
+          u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host side
+
+constexpr int kTlNWV = 8;  // waves per block
+constexpr int kTlMG = 4;   // groups of 16 tokens per block
+
+template <int WF, int NMAT, int TPW>
+static int launch_tiled(const TlParams& p, hipStream_t s) {
+  const int nbn = p.N / (kTlNWV * TPW * kTileRows);
+  const size_t lds = (size_t)3 * kTlMG * 2048;
+  hipLaunchKernelGGL((tiled_kernel<WF, NMAT, TPW, kTlMG, kTlNWV>), dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s, p);
+  return check_launch("tiled_kernel");
+}
+
+// Tiles per wave: gate/up 2 per matrix (a block covers 256 features); down 4 when the features
+// divide into 512-row blocks, else 2.
+static int down_tpw(int H) { return H % (kTlNWV * 4 * kTileRows) == 0 ? 4 : 2; }
+
+bool tiled_supported(int M, int H, int I) {
+  return M >= 1 && I % (kTlNWV * 2 * kTileRows) == 0 && H % (kTlNWV * 2 * kTileRows) == 0;
+}
+
+int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
+  (void)num_cus;
+  if (!tiled_supported(a.M, a.H, a.I)) return set_error(-1, "tiled path: H=%d I=%d not multiples of 256", a.H, a.I);
+  const WsLayout L = ws_layout(a.M, a.H, a.I, a.fmt);
+  const int fmt = a.fmt;
+  int* tx = (int*)(a.ws + L.tx);
+  int* th = (int*)(a.ws + L.th);
+  uint16_t* x16 = (uint16_t*)(a.ws + L.x16);
+  uint16_t* h = (uint16_t*)(a.ws + L.h);
+  profile_mark(0, s);
+  if (fmt == 1) {
+    int rc = launch_prep(a, s);
+    if (rc) return rc;
+  }
+  profile_mark(1, s);
+  const int nbm = (a.M + kTlMG * 16 - 1) / (kTlMG * 16);
+  TlParams g{};
+  g.w0 = a.wg;
+  g.w1 = a.wu;
+  g.rowexp0 = (const int*)(a.wg + rowexp_offset(a.I, a.H, fmt));
+  g.rowexp1 = (const int*)(a.wu + rowexp_offset(a.I, a.H, fmt));
+  g.src = fmt == 1 ? x16 : (const uint16_t*)a.x;
+  g.M = a.M;
+  g.K = a.H;
+  g.N = a.I;
+  g.C = a.H / kSuperK;
+  g.nbm = nbm;
+  g.tsrc = tx;
+  g.tout = th;
+  g.out = h;
+  int rc = fmt == 1 ? launch_tiled<1, 2, 2>(g, s) : launch_tiled<0, 2, 2>(g, s);
+  if (rc) return rc;
+  profile_mark(2, s);
+  TlParams d{};
+  d.w0 = a.wd;
+  d.rowexp0 = (const int*)(a.wd + rowexp_offset(a.H, a.I, fmt));
+  d.src = h;
+  d.M = a.M;
+  d.K = a.I;
+  d.N = a.H;
+  d.C = a.I / kSuperK;
+  d.nbm = nbm;
+  d.tsrc = th;
+  d.out = a.out;
+  d.residual = a.residual;
+  d.out_f32 = a.out_f32;
+  d.res_f32 = a.res_f32;
+  if (down_tpw(a.H) == 4)
+    rc = fmt == 1 ? launch_tiled<1, 1, 4>(d, s) : launch_tiled<0, 1, 4>(d, s);
+  else
+    rc = fmt == 1 ? launch_tiled<1, 1, 2>(d, s) : launch_tiled<0, 1, 2>(d, s);
+  if (rc) return rc;
+  profile_mark(3, s);
+  return 0;
+}
+
+}  // namespace qmlp

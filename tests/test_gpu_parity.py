@@ -280,3 +280,24 @@ def test_shape_errors(pkg, cuda):
         mlp.forward(torch.zeros((2, 1024), dtype=torch.bfloat16))
     with pytest.raises(ValueError):
         pkg.pack_weight(torch.zeros((17, 256), dtype=torch.bfloat16, device=cuda))
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+@pytest.mark.parametrize("H,I,M", [(1024, 3072, 2048), (5120, 17408, 256), (1024, 3072, 200)])
+def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
+    """Many-token forwards (the LDS-tiled matrix-core kernels): a full 2048-token chunk, the 27B
+    shape, and a token count that leaves a partial token block."""
+    import torch
+    from qwen_mlp_amd import workloads
+
+    print(f"case prefill {fmt} H={H} I={I} M={M}", flush=True)
+    sd = workloads.state_dict(H, I, layer=8, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=M)
+    x = workloads.activations(M, H, seed=4242 + M, gain=False, device=cuda)
+    y32 = mlp.forward(x, residual=x, out_dtype=torch.float32)
+    y16 = mlp.forward(x, residual=x)
+    torch.cuda.synchronize()
+    assert torch.equal(y32.to(torch.bfloat16), y16)
+    hw = _host_weights(pkg, sd, fmt)
+    xf = x.float().cpu().numpy()
+    _check(y32.cpu().numpy(), _oracle(xf, hw), f"prefill {fmt} H={H} I={I} M={M}")
