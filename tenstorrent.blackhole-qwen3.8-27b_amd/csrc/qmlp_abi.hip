@@ -235,8 +235,11 @@ int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* w
   if (int rc = current_device_info(&di)) return rc;
   ForwardArgs a{x, (const uint8_t*)wg, (const uint8_t*)wu, (const uint8_t*)wd, residual, out, (uint8_t*)ws,
                 M, H, I, fmt, (flags & QMLP_OUT_F32) ? 1 : 0, (flags & QMLP_RESIDUAL_F32) ? 1 : 0};
+  // M <= 16: split-K weight streaming with LDS-staged activations; M <= 32: stream-K weight
+  // streaming with activations read from L2; larger M: the LDS-tiled matrix-core GEMM.
   if (gemv_supported(M, H, I, di.num_cus)) return launch_forward_gemv(a, di.num_cus, (hipStream_t)stream);
-  if (M > 32 && tiled_supported(M, H, I)) return launch_forward_tiled(a, di.num_cus, (hipStream_t)stream);
+  if (stream_supported(M, H, I, di.num_cus)) return launch_forward_stream(a, di.num_cus, (hipStream_t)stream);
+  if (tiled_supported(M, H, I)) return launch_forward_tiled(a, di.num_cus, (hipStream_t)stream);
   return launch_forward_skinny(a, di.num_cus, (hipStream_t)stream);
 }
 

@@ -114,6 +114,26 @@ __device__ __forceinline__ void dq16(u32x4 w, f16x2 s, f16x8& a0, f16x8& a1) {
   a1 = f16x8{p4.x, p4.y, p5.x, p5.y, p6.x, p6.y, p7.x, p7.y};
 }
 
+// The same 16 mantissas -> two bf16 x8 operands, exactly: (u - 128) * s has at most 8 significant
+// bits, s = 2^(E5 - 15) from the exponent byte E5 << 2 (group scale before the row exponent).
+__device__ __forceinline__ void dq16_bf16(u32x4 w, uint32_t ebyte, bf16x8& a0, bf16x8& a1) {
+  const float s = __uint_as_float(((ebyte >> 2) + 112u) << 23);
+  const float c = -128.0f * s;
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t d = w[i];
+    const float f0 = __builtin_fmaf((float)(d & 0xffu), s, c);
+    const float f1 = __builtin_fmaf((float)((d >> 8) & 0xffu), s, c);
+    const float f2 = __builtin_fmaf((float)((d >> 16) & 0xffu), s, c);
+    const float f3 = __builtin_fmaf((float)(d >> 24), s, c);
+    o[2 * i] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);  // high halves
+    o[2 * i + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+  }
+  a0 = __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+  a1 = __builtin_bit_cast(bf16x8, u32x4{o[4], o[5], o[6], o[7]});
+}
+
 // Logical workgroup index so that consecutive logical indices share an XCD (hardware dispatches
 // workgroup b to XCD b % 8): each XCD then streams one contiguous eighth of the weights and
 // neighbouring workgroups that share a tile exchange partial sums through the same L2.

@@ -78,5 +78,9 @@ int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s);
 int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s);
 bool tiled_supported(int M, int H, int I);
 int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s);
+// Stream-K weight-streaming kernels for M <= 32 (qmlp_stream.hip).
+int plan_stream(int rows, int K, int num_cus, int* P, int* maxseg);
+bool stream_supported(int M, int H, int I, int num_cus);
+int launch_forward_stream(const ForwardArgs& a, int num_cus, hipStream_t s);
 
 }  // namespace qmlp
