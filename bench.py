@@ -36,7 +36,7 @@ def parse():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="qwen3-27b-mlp-m16-bfp8")
     ap.add_argument("--rotate", type=int, default=8, help="distinct layers cycled through by the timed loop")
     ap.add_argument("--no-extras", action="store_true", help="skip the bf16 variant, sweep, stack and prefill")

@@ -134,6 +134,15 @@ __device__ __forceinline__ void dq16_bf16(u32x4 w, uint32_t ebyte, bf16x8& a0, b
   a1 = __builtin_bit_cast(bf16x8, u32x4{o[4], o[5], o[6], o[7]});
 }
 
+// LDS layout of the matrix-core B operand, 2 KB per 64-K step of 16 token rows.  Lane
+// l = 16 q + rr needs K = 16 q + 8 h + (0..7) of token row rr for its two products (h = 0, 1).
+// The halves live in separate 1 KB blocks and inside a block the lane's 16-byte slot is rotated
+// by 2 q + h: every 16-lane read and the 8 chunks that fill one token row's step land in distinct
+// bank groups.
+__host__ __device__ inline uint32_t bfrag_off(int q, int rr, int h) {
+  return (uint32_t)(h * 1024 + (q * 16 + ((rr + 2 * q + h) & 15)) * 16);
+}
+
 // Logical workgroup index so that consecutive logical indices share an XCD (hardware dispatches
 // workgroup b to XCD b % 8): each XCD then streams one contiguous eighth of the weights and
 // neighbouring workgroups that share a tile exchange partial sums through the same L2.

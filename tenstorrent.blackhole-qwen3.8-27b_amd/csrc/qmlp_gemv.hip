@@ -62,9 +62,9 @@ struct GStage {
 
 // ---------------------------------------------------------------- staging of the B operand
 //
-// LDS layout: for each K-step kk of the workgroup's K range, 64 lanes x 32 bytes: lane
-// l = 16 * quarter + m holds the 16 values K = 64 kk + 16 quarter + (0..15) of token row m, so the
-// main loop reads its B operand with two conflict-free 16-byte LDS loads per K-step.
+// LDS layout: for each K-step kk of the workgroup's K range, 2 KB in bfrag_off order (lane
+// l = 16 * quarter + m reads the 16 values K = 64 kk + 16 quarter + (0..15) of token row m as two
+// conflict-free 16-byte LDS loads).
 //
 // Staging is split in two so that the activation loads are issued before the first weight
 // loads (vector loads complete in order: waiting for activations issued after the weights would
@@ -92,10 +92,9 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, const BStage<N
   constexpr int TPR = NW * 64 / 16;
   const int m = threadIdx.x / TPR, tl = threadIdx.x % TPR;
   const int nch = p.KQ * kSuperK / (TPR * 8);
-  auto lds_off = [&](int e) {
+  auto lds_off = [&](int e) {  // K offset e of token row m inside the workgroup's range
     const int kk = e >> 6, r = e & 63;
-    const int l = (r >> 4) * 16 + m;
-    return ((kk * 64 + l) * 2 + ((r >> 3) & 1)) * 16;
+    return kk * 2048 + (int)bfrag_off(r >> 4, m, (r >> 3) & 1);
   };
   if (!p.x_scale) {
 #pragma unroll
@@ -213,9 +212,9 @@ __device__ __forceinline__ void gcompute(const GStage<WF, NMAT, SPS>& st, const 
 #pragma unroll
   for (int jj = 0; jj < SPS; ++jj) {
     const int j = q.part * SPS + jj;
-    const uint8_t* bp = ldsb + ((q.s * kSteps + j) * 64 + lane) * 32;
-    const u32x4 b0 = *(const u32x4*)bp;
-    const u32x4 b1 = *(const u32x4*)(bp + 16);
+    const uint8_t* bp = ldsb + (q.s * kSteps + j) * 2048;
+    const u32x4 b0 = *(const u32x4*)(bp + bfrag_off(lane >> 4, lane & 15, 0));
+    const u32x4 b1 = *(const u32x4*)(bp + bfrag_off(lane >> 4, lane & 15, 1));
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) {
       if constexpr (WF) {

@@ -9,8 +9,8 @@
 // each wave owns TPW 16-row tiles of each matrix and streams them through registers in the packed
 // layout (bfp8 dequantised exactly to fp16 in registers, bf16 used as is).  The tokens are the
 // B operand: a block stages MG groups of 16 token rows, one 64-K step at a time, into a 3-slot LDS
-// ring shared by all its waves (the same lane order as the weight-streaming kernels, so each lane
-// reads its B fragment with two 16-byte LDS loads).  One block = NWV waves x TPW tiles x NMAT
+// ring shared by all its waves (bfrag_off's bank-conflict-free order, the same as the
+// weight-streaming kernels', so each lane reads its B fragment with two 16-byte LDS loads).  One block = NWV waves x TPW tiles x NMAT
 // matrices of features by MG x 16 tokens; every A fragment feeds MG x 2 products and every B
 // fragment NMAT x TPW x 2.
 //
@@ -73,7 +73,7 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
     const int c = threadIdx.x + i * NT, r = c >> 3, j = c & 7;
     const int mr = min(m0 + r, p.M - 1);
     goff[i] = (uint32_t)(mr * p.K + j * 8) * 2u;
-    loff[i] = (uint32_t)((r >> 4) * 2048 + (((j >> 1) * 16 + (r & 15)) * 2 + (j & 1)) * 16);
+    loff[i] = (uint32_t)(r >> 4) * 2048u + bfrag_off(j >> 1, r & 15, j & 1);
   }
   const uint8_t* srcb = (const uint8_t*)p.src;
   auto bload = [&](u32x4(&v)[CPT], int step) {
@@ -120,8 +120,9 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
 #pragma unroll
       for (int g = 0; g < MG; ++g) acc[mat][t][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  const uint32_t boff0 = bfrag_off(lane >> 4, lane & 15, 0), boff1 = bfrag_off(lane >> 4, lane & 15, 1);
   auto compute = [&](const TlStage<WF, NMAT, TPW>& st, int step) {
-    const uint8_t* slot = lds + (step % 3) * SLOT + lane * 32;
+    const uint8_t* slot = lds + (step % 3) * SLOT;
     if constexpr (WF) {
       f16x8 a[NMAT][TPW][2];
 #pragma unroll
@@ -130,8 +131,8 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
         for (int t = 0; t < TPW; ++t) dq16(st.w[mat][t][0], scale_pair(st.e[mat][t], step & 3), a[mat][t][0], a[mat][t][1]);
 #pragma unroll
       for (int g = 0; g < MG; ++g) {
-        const f16x8 b0 = __builtin_bit_cast(f16x8, *(const u32x4*)(slot + g * 2048));
-        const f16x8 b1 = __builtin_bit_cast(f16x8, *(const u32x4*)(slot + g * 2048 + 16));
+        const f16x8 b0 = __builtin_bit_cast(f16x8, *(const u32x4*)(slot + g * 2048 + boff0));
+        const f16x8 b1 = __builtin_bit_cast(f16x8, *(const u32x4*)(slot + g * 2048 + boff1));
 #pragma unroll
         for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
@@ -143,8 +144,8 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
     } else {
 #pragma unroll
       for (int g = 0; g < MG; ++g) {
-        const bf16x8 b0 = __builtin_bit_cast(bf16x8, *(const u32x4*)(slot + g * 2048));
-        const bf16x8 b1 = __builtin_bit_cast(bf16x8, *(const u32x4*)(slot + g * 2048 + 16));
+        const bf16x8 b0 = __builtin_bit_cast(bf16x8, *(const u32x4*)(slot + g * 2048 + boff0));
+        const bf16x8 b1 = __builtin_bit_cast(bf16x8, *(const u32x4*)(slot + g * 2048 + boff1));
 #pragma unroll
         for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
@@ -263,9 +264,9 @@ static int launch_tiled(const TlParams& p, hipStream_t s) {
   return check_launch("tiled_kernel");
 }
 
-// Tiles per wave: gate/up 2 per matrix (a block covers 256 features); down 4 when the features
-// divide into 512-row blocks, else 2.
-static int down_tpw(int H) { return H % (kTlNWV * 4 * kTileRows) == 0 ? 4 : 2; }
+// Tiles per wave: 2 per matrix for both projections (a block covers 256 features; for the down
+// projection that gives 4x more blocks than 4 tiles per wave, which balances the CUs better than
+// the extra B-fragment reuse would gain).
 
 bool tiled_supported(int M, int H, int I) {
   return M >= 1 && I % (kTlNWV * 2 * kTileRows) == 0 && H % (kTlNWV * 2 * kTileRows) == 0;
@@ -318,10 +319,7 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.residual = a.residual;
   d.out_f32 = a.out_f32;
   d.res_f32 = a.res_f32;
-  if (down_tpw(a.H) == 4)
-    rc = fmt == 1 ? launch_tiled<1, 1, 4>(d, s) : launch_tiled<0, 1, 4>(d, s);
-  else
-    rc = fmt == 1 ? launch_tiled<1, 1, 2>(d, s) : launch_tiled<0, 1, 2>(d, s);
+  rc = fmt == 1 ? launch_tiled<1, 1, 2>(d, s) : launch_tiled<0, 1, 2>(d, s);
   if (rc) return rc;
   profile_mark(3, s);
   return 0;
