@@ -123,6 +123,24 @@ int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* w
                     const void* residual, void* out, void* ws, size_t ws_bytes, int M, int H, int I,
                     int fmt, int flags, qmlp_stream_t stream);
 
+/* The decoder's feed-forward half with its RMSNorm prologue:
+ *
+ *   out = h + down( silu(gate(n)) * up(n) ),   n = h / sqrt(mean(h^2) + eps) * (1 + norm_w)
+ *
+ * (the zero-centred RMSNorm, mean over H).  Replaces ff_input = self.ffn_norm(h);
+ * ff_output = self.feed_forward.forward(ff_input); output = ttnn.add(h, ff_output)
+ * (docker/qwen-c2-graft/graft/layer.py:352-357; the norm is the framework RMSNorm with
+ * add_unit_offset, layer.py:110-112,228-237).
+ *   h       bf16 [M, H], the pre-norm hidden state (also the residual)
+ *   norm_w  bf16 [H]
+ *   out     bf16 [M, H] (fp32 with QMLP_OUT_F32); may equal h (in-place residual update)
+ * Other arguments and constraints as qmlp_forward_ex (QMLP_RESIDUAL_F32 is not accepted).  M <= 16
+ * fuses the norm into the gate/up kernel (the channel gain into the activation staging, the
+ * per-token 1/rms into the epilogue); larger M run it as one extra pass over h. */
+int qmlp_forward_rmsnorm(const void* h, const void* norm_w, float eps, const void* wg, const void* wu,
+                         const void* wd, void* out, void* ws, size_t ws_bytes, int M, int H, int I,
+                         int fmt, int flags, qmlp_stream_t stream);
+
 /* Workspace bytes needed by qmlp_forward for these sizes (host only, no GPU needed). */
 size_t qmlp_workspace_bytes(int M, int H, int I, int fmt);
 

@@ -54,6 +54,31 @@ def swiglu_torch(x, wg, wu, wd, residual=None):
     return y
 
 
+def rmsnorm(x, weight, eps=1e-6):
+    """Zero-centred RMSNorm of each row in float32: ``x / sqrt(mean(x^2) + eps) * (1 + weight)``.
+
+    The decoder's ``ffn_norm`` is the framework RMSNorm with ``add_unit_offset=True`` (the ``+1`` on
+    the stored weight, ``docker/qwen-c2-graft/graft/layer.py:110-112,228-237``); the mean runs over
+    the hidden dimension.  x: [M, H]; weight: [H].
+    """
+    x = np.asarray(x, dtype=np.float32)
+    w = np.asarray(weight, dtype=np.float32)
+    ms = np.mean(x.astype(np.float64) ** 2, axis=1, keepdims=True)
+    rstd = (1.0 / np.sqrt(ms + eps)).astype(np.float32)
+    return (x * rstd * (np.float32(1) + w)).astype(np.float32)
+
+
+def norm_swiglu(h, norm_weight, wg, wu, wd, eps=1e-6):
+    """The decoder's feed-forward half: ``h + down(silu(gate(n)) * up(n))`` with
+    ``n = bf16(rmsnorm(h))`` -- the norm's output is a bf16 tensor that the MLP consumes
+    (``layer.py:352-357``).  Returns float32 [M, H]."""
+    from . import bf16 as obf16
+
+    n = rmsnorm(h, norm_weight, eps)
+    n = obf16.round_f32(n)
+    return swiglu(n, wg, wu, wd, residual=h)
+
+
 def tolerance_ok(actual, expected, rel=1e-2):
     """Parity bar: ``max|actual - expected| <= rel * RMS(expected)``.  Returns (ok, err, bound)."""
     actual = np.asarray(actual, dtype=np.float64)

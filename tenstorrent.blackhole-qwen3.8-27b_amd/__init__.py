@@ -12,6 +12,7 @@ from .mlp import (
     dequantize,
     load_mlp_weights,
     mlp_forward,
+    mlp_forward_rmsnorm,
     new_workspace,
     pack_canonical_bfp8,
     pack_weight,
@@ -22,6 +23,6 @@ from .mlp import (
 
 __all__ = [
     "FMT_BF16", "FMT_BFP8", "LIB_PATH", "QmlpError", "lib", "MLPWeights", "PackedWeight", "Qwen36MLP",
-    "dequantize", "load_mlp_weights", "mlp_forward", "new_workspace", "pack_canonical_bfp8", "pack_weight",
+    "dequantize", "load_mlp_weights", "mlp_forward", "mlp_forward_rmsnorm", "new_workspace", "pack_canonical_bfp8", "pack_weight",
     "quantize_bfp8", "unpack_bfp8", "workspace_bytes",
 ]

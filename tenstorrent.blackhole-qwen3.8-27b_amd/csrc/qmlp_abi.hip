@@ -71,7 +71,9 @@ WsLayout ws_layout(int M, int H, int I, int fmt) {
   L.part_d = off;
   off = align256(off + std::max(sk_d, gv_d));
   L.pss = off;
-  off = align256(off + (size_t)kMaxWorkgroups * 16 * 4);
+  off = align256(off + (size_t)kMaxWorkgroups * 32 * 4);
+  L.xn = off;  // bf16 [M, H]: the normalised activations when the RMSNorm runs as its own pass
+  off = align256(off + (size_t)M * H * 2);
   L.total = off;
   return L;
 }
@@ -206,41 +208,67 @@ int qmlp_workspace_init(void* ws, size_t ws_bytes, qmlp_stream_t stream) {
   return launch_fill_zero(ws, ws_bytes, (hipStream_t)stream);
 }
 
-int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* wd, const void* residual, void* out,
-                    void* ws, size_t ws_bytes, int M, int H, int I, int fmt, int flags, qmlp_stream_t stream) {
-  if (!x || !wg || !wu || !wd || !out || !ws) return set_error(QMLP_E_NULL, "qmlp_forward: null pointer");
-  if (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8) return set_error(QMLP_E_FORMAT, "qmlp_forward: unknown format %d", fmt);
-  if (flags & ~(QMLP_OUT_F32 | QMLP_RESIDUAL_F32)) return set_error(QMLP_E_FORMAT, "qmlp_forward: unknown flags 0x%x", flags);
-  if (M < 1 || M > 65536) return set_error(QMLP_E_SHAPE, "qmlp_forward: M=%d out of range [1, 65536]", M);
+// Shared validation and dispatch of the forward entry points.
+static int forward_impl(const char* fn, const void* x, const void* wg, const void* wu, const void* wd,
+                        const void* residual, void* out, void* ws, size_t ws_bytes, int M, int H, int I, int fmt,
+                        int flags, const void* normw, float eps, qmlp_stream_t stream) {
+  if (!x || !wg || !wu || !wd || !out || !ws) return set_error(QMLP_E_NULL, "%s: null pointer", fn);
+  if (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8) return set_error(QMLP_E_FORMAT, "%s: unknown format %d", fn, fmt);
+  if (flags & ~(QMLP_OUT_F32 | QMLP_RESIDUAL_F32)) return set_error(QMLP_E_FORMAT, "%s: unknown flags 0x%x", fn, flags);
+  if (M < 1 || M > 65536) return set_error(QMLP_E_SHAPE, "%s: M=%d out of range [1, 65536]", fn, M);
   if (!shape_ok(16, H) || !shape_ok(16, I))
-    return set_error(QMLP_E_SHAPE, "qmlp_forward: H=%d and I=%d must be positive multiples of 256", H, I);
+    return set_error(QMLP_E_SHAPE, "%s: H=%d and I=%d must be positive multiples of 256", fn, H, I);
   if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(ws) ||
-      (residual && !aligned16(residual)))
-    return set_error(QMLP_E_ALIGN, "qmlp_forward: every pointer must be 16-byte aligned");
+      (residual && !aligned16(residual)) || (normw && !aligned16(normw)))
+    return set_error(QMLP_E_ALIGN, "%s: every pointer must be 16-byte aligned", fn);
+  if (normw && !(eps >= 0.0f)) return set_error(QMLP_E_SHAPE, "%s: eps must be >= 0", fn);
   const size_t xbytes = (size_t)M * H * 2, obytes = (size_t)M * H * ((flags & QMLP_OUT_F32) ? 4 : 2);
   const uintptr_t xb = (uintptr_t)x, ob = (uintptr_t)out;
-  if (xb < ob + obytes && ob < xb + xbytes) return set_error(QMLP_E_SHAPE, "qmlp_forward: out must not overlap x");
+  if (!(normw && x == out) && xb < ob + obytes && ob < xb + xbytes)
+    return set_error(QMLP_E_SHAPE, "%s: out must not overlap x", fn);
   if (residual && residual != out) {
     const size_t rbytes = (size_t)M * H * ((flags & QMLP_RESIDUAL_F32) ? 4 : 2);
     const uintptr_t rb = (uintptr_t)residual;
     if (rb < ob + obytes && ob < rb + rbytes)
-      return set_error(QMLP_E_SHAPE, "qmlp_forward: out may equal residual but must not partially overlap it");
+      return set_error(QMLP_E_SHAPE, "%s: out may equal residual but must not partially overlap it", fn);
   }
   if (residual == out && residual && ((flags & QMLP_OUT_F32) != 0) != ((flags & QMLP_RESIDUAL_F32) != 0))
-    return set_error(QMLP_E_SHAPE, "qmlp_forward: an in-place residual needs the same dtype as out");
+    return set_error(QMLP_E_SHAPE, "%s: an in-place residual needs the same dtype as out", fn);
   const WsLayout L = ws_layout(M, H, I, fmt);
   if (ws_bytes < L.total)
-    return set_error(QMLP_E_WORKSPACE, "qmlp_forward: workspace holds %zu bytes, needs %zu", ws_bytes, L.total);
+    return set_error(QMLP_E_WORKSPACE, "%s: workspace holds %zu bytes, needs %zu", fn, ws_bytes, L.total);
   DeviceInfo di;
   if (int rc = current_device_info(&di)) return rc;
   ForwardArgs a{x, (const uint8_t*)wg, (const uint8_t*)wu, (const uint8_t*)wd, residual, out, (uint8_t*)ws,
-                M, H, I, fmt, (flags & QMLP_OUT_F32) ? 1 : 0, (flags & QMLP_RESIDUAL_F32) ? 1 : 0};
-  // M <= 16: split-K weight streaming with LDS-staged activations; M <= 32: stream-K weight
-  // streaming with activations read from L2; larger M: the LDS-tiled matrix-core GEMM.
+                M, H, I, fmt, (flags & QMLP_OUT_F32) ? 1 : 0, (flags & QMLP_RESIDUAL_F32) ? 1 : 0, normw, eps};
+  // M <= 16: split-K weight streaming with LDS-staged activations (the RMSNorm fused into its
+  // staging and epilogue); M <= 32: stream-K weight streaming with activations read from L2;
+  // larger M: the LDS-tiled matrix-core GEMM.  The last two take the RMSNorm as a separate pass.
   if (gemv_supported(M, H, I, di.num_cus)) return launch_forward_gemv(a, di.num_cus, (hipStream_t)stream);
+  if (normw) {
+    uint8_t* xn = (uint8_t*)ws + L.xn;
+    if (int rc = launch_rmsnorm(x, normw, eps, M, H, xn, (hipStream_t)stream)) return rc;
+    a.x = xn;
+    a.normw = nullptr;
+  }
   if (stream_supported(M, H, I, di.num_cus)) return launch_forward_stream(a, di.num_cus, (hipStream_t)stream);
   if (tiled_supported(M, H, I)) return launch_forward_tiled(a, di.num_cus, (hipStream_t)stream);
   return launch_forward_skinny(a, di.num_cus, (hipStream_t)stream);
+}
+
+int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* wd, const void* residual, void* out,
+                    void* ws, size_t ws_bytes, int M, int H, int I, int fmt, int flags, qmlp_stream_t stream) {
+  return forward_impl("qmlp_forward", x, wg, wu, wd, residual, out, ws, ws_bytes, M, H, I, fmt, flags, nullptr, 0.0f,
+                      stream);
+}
+
+int qmlp_forward_rmsnorm(const void* h, const void* norm_w, float eps, const void* wg, const void* wu, const void* wd,
+                         void* out, void* ws, size_t ws_bytes, int M, int H, int I, int fmt, int flags,
+                         qmlp_stream_t stream) {
+  if (!norm_w) return set_error(QMLP_E_NULL, "qmlp_forward_rmsnorm: null norm weight");
+  if (flags & QMLP_RESIDUAL_F32) return set_error(QMLP_E_FORMAT, "qmlp_forward_rmsnorm: the residual is h (bf16)");
+  return forward_impl("qmlp_forward_rmsnorm", h, wg, wu, wd, h, out, ws, ws_bytes, M, H, I, fmt, flags, norm_w, eps,
+                      stream);
 }
 
 int qmlp_forward(const void* x, const void* wg, const void* wu, const void* wd, const void* residual, void* out,

@@ -42,6 +42,8 @@ struct GvParams {
   int M, K, N;
   int C, T, G, S, KQ, Ng, P, maxseg;
   int x_scale;            // 1: src is bf16 and is converted to fp16 * 2^t (bfp8 gate/up)
+  const uint16_t* normw;  // gate/up with the RMSNorm prologue: bf16 [K] weight w (gain 1 + w)
+  float eps;              //   and its epsilon
   const int* th_in;       // bfp8 down: h = h16 * 2^-th[m]
   int* th_out;            // bfp8 gate/up: th[m] written by tile group 0
   const Trailer* tg;      // bfp8 gate/up: weight row-norm trailers for the h bound
@@ -50,7 +52,8 @@ struct GvParams {
   const void* residual;   // down: [M, N] bf16 or fp32, may alias out
   int out_f32, res_f32;
   float* part;            // [P][G][NMAT * 64] f32x4 partial slots
-  float* pss;             // [P][16] per-workgroup token sum of squares (bfp8 gate/up)
+  float* pss;             // [P][32] per-workgroup token sums: [0,16) of the staged values'
+                          // squares (bfp8 h bound), [16,32) of the raw x squares (RMSNorm)
   int* counters;          // [Ng] arrival counters (left at zero)
 };
 
@@ -70,13 +73,14 @@ struct GStage {
 // loads (vector loads complete in order: waiting for activations issued after the weights would
 // also wait for the weights).  Thread (m = token row, tl) handles chunks of 8 values at
 // K = 8 * (tl + c * TPR), c < nch = KQ; all MAXCH loads are unconditional (clamped chunk index).
-template <int NW, int MAXCH>
+template <int NW, int MAXCH, bool NORM>
 struct BStage {
   u32x4 v[MAXCH];
+  u32x4 w[NORM ? MAXCH : 1];  // RMSNorm weight of the same K values
 };
 
-template <int NW, int MAXCH>
-__device__ __forceinline__ void stage_b_issue(const GvParams& p, int k0, BStage<NW, MAXCH>& bs) {
+template <int NW, int MAXCH, bool NORM>
+__device__ __forceinline__ void stage_b_issue(const GvParams& p, int k0, BStage<NW, MAXCH, NORM>& bs) {
   constexpr int TPR = NW * 64 / 16;  // threads per token row
   const int m = threadIdx.x / TPR, tl = threadIdx.x % TPR;
   const int mr = min(m, p.M - 1);  // rows beyond M duplicate row M-1 (their outputs are discarded)
@@ -84,11 +88,17 @@ __device__ __forceinline__ void stage_b_issue(const GvParams& p, int k0, BStage<
   const uint16_t* row = p.src + (size_t)mr * p.K + k0;
 #pragma unroll
   for (int c = 0; c < MAXCH; ++c) bs.v[c] = *(const u32x4*)(row + (tl + min(c, nch - 1) * TPR) * 8);
+  if constexpr (NORM) {
+#pragma unroll
+    for (int c = 0; c < MAXCH; ++c) bs.w[c] = *(const u32x4*)(p.normw + k0 + (tl + min(c, nch - 1) * TPR) * 8);
+  }
 }
 
-template <int NW, int MAXCH>
-__device__ __forceinline__ void stage_b_finish(const GvParams& p, const BStage<NW, MAXCH>& bs, uint8_t* ldsb,
-                                               int* lds_t, float* lds_ss) {
+// With the RMSNorm prologue the staged value is x * (1 + w) (the per-token 1/rms is a scale of
+// the whole product and is applied in the epilogue), rounded once to the B operand's type.
+template <int NW, int MAXCH, bool NORM>
+__device__ __forceinline__ void stage_b_finish(const GvParams& p, const BStage<NW, MAXCH, NORM>& bs, uint8_t* ldsb,
+                                               int* lds_t, float* lds_ss, float* lds_sx) {
   constexpr int TPR = NW * 64 / 16;
   const int m = threadIdx.x / TPR, tl = threadIdx.x % TPR;
   const int nch = p.KQ * kSuperK / (TPR * 8);
@@ -96,24 +106,38 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, const BStage<N
     const int kk = e >> 6, r = e & 63;
     return kk * 2048 + (int)bfrag_off(r >> 4, m, (r >> 3) & 1);
   };
-  if (!p.x_scale) {
+  if (!p.x_scale && !NORM) {
 #pragma unroll
     for (int c = 0; c < MAXCH; ++c)
       if (c < nch) *(u32x4*)(ldsb + lds_off((tl + c * TPR) * 8)) = bs.v[c];
     return;
   }
-  // bf16 -> fp16 * 2^t with max|x| * 2^t in [2^14, 2^15) over this K range (exact unless a value
-  // is 2^31 times smaller than the range maximum).  Also the range's sum of squares for th.
-  float mx = 0.f, ss = 0.f;
+  auto value = [&](int c, int i, int hi, float& xr) {
+    const uint32_t xw = hi ? bs.v[c][i] >> 16 : bs.v[c][i] & 0xffffu;
+    xr = bf16_to_f32((uint16_t)xw);
+    if constexpr (NORM) {
+      const uint32_t ww = hi ? bs.w[c][i] >> 16 : bs.w[c][i] & 0xffffu;
+      return __builtin_fmaf(xr, bf16_to_f32((uint16_t)ww), xr);
+    }
+    return xr;
+  };
+  // bfp8: value -> fp16 * 2^t with max|value| * 2^t in [2^14, 2^15) over this K range (exact
+  // unless a value is 2^31 times smaller than the range maximum).  The range's sums of squares
+  // feed the h bound (values) and the RMSNorm (raw x).
+  float mx = 0.f, ss = 0.f, sx = 0.f;
 #pragma unroll
   for (int c = 0; c < MAXCH; ++c) {
     if (c < nch) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float a = bf16_to_f32((uint16_t)(bs.v[c][i] & 0xffffu)), b = bf16_to_f32((uint16_t)(bs.v[c][i] >> 16));
-        mx = fmaxf(mx, fmaxf(fabsf(a), fabsf(b)));
-        ss = fmaf(a, a, ss);
-        ss = fmaf(b, b, ss);
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+          float xr;
+          const float v = value(c, i, hi, xr);
+          mx = fmaxf(mx, fabsf(v));
+          ss = fmaf(v, v, ss);
+          if constexpr (NORM) sx = fmaf(xr, xr, sx);
+        }
       }
     }
   }
@@ -122,13 +146,15 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, const BStage<N
   for (int o = TPR / 2; o > 0; o >>= 1) {
     mx = fmaxf(mx, __shfl_xor(mx, o));
     ss += __shfl_xor(ss, o);
+    if constexpr (NORM) sx += __shfl_xor(sx, o);
   }
   int e2 = 0;
   if (mx > 0.f) frexpf(mx, &e2);
-  const int t = mx > 0.f ? 15 - e2 : 0;
+  const int t = (p.x_scale && mx > 0.f) ? 15 - e2 : 0;
   if (tl == 0) {
     lds_t[m] = t;
     lds_ss[m] = ss;
+    lds_sx[m] = sx;
   }
 #pragma unroll
   for (int c = 0; c < MAXCH; ++c) {
@@ -136,9 +162,13 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, const BStage<N
       uint32_t o[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float a = __builtin_amdgcn_ldexpf(bf16_to_f32((uint16_t)(bs.v[c][i] & 0xffffu)), t);
-        const float b = __builtin_amdgcn_ldexpf(bf16_to_f32((uint16_t)(bs.v[c][i] >> 16)), t);
-        o[i] = (uint32_t)f32_to_f16_bits(a) | ((uint32_t)f32_to_f16_bits(b) << 16);
+        float xr;
+        const float a = value(c, i, 0, xr), b = value(c, i, 1, xr);
+        if (p.x_scale)
+          o[i] = (uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(a, t)) |
+                 ((uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(b, t)) << 16);
+        else
+          o[i] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
       }
       *(u32x4*)(ldsb + lds_off((tl + c * TPR) * 8)) = u32x4{o[0], o[1], o[2], o[3]};
     }
@@ -237,7 +267,8 @@ __device__ __forceinline__ void gcompute(const GStage<WF, NMAT, SPS>& st, const 
 // Lane l holds rows 4*(l/16) + v (v = 0..3) of token column m = l % 16 -- the 16x16 matrix-core
 // output layout.
 template <int WF, int NMAT>
-__device__ __forceinline__ void gepilogue(const GvParams& p, int t, const f32x4 (&tot)[NMAT], int lane, int th) {
+__device__ __forceinline__ void gepilogue(const GvParams& p, int t, const f32x4 (&tot)[NMAT], int lane, int th,
+                                          float rs) {
   const int m = lane & 15;
   if (m >= p.M) return;
   const int nb = t * kTileRows + (lane >> 4) * 4;
@@ -245,7 +276,7 @@ __device__ __forceinline__ void gepilogue(const GvParams& p, int t, const f32x4 
   if constexpr (NMAT == 2) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      float g = tot[0][v], u = tot[1][v];
+      float g = tot[0][v] * rs, u = tot[1][v] * rs;  // rs: the token's 1/rms (1 without the norm)
       if constexpr (WF) {
         g = __builtin_amdgcn_ldexpf(g, p.rowexp0[nb + v]);
         u = __builtin_amdgcn_ldexpf(u, p.rowexp1[nb + v]);
@@ -288,7 +319,7 @@ __device__ __forceinline__ void gepilogue(const GvParams& p, int t, const f32x4 
 
 // ---------------------------------------------------------------- kernel
 
-template <int WF, int NMAT, int NW, int MAXCH>
+template <int WF, int NMAT, int NW, int MAXCH, bool NORM>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
   constexpr int SPS = WF ? 4 : 2;  // K-steps per register stage
   constexpr int SPU = kSteps / SPS;
@@ -296,6 +327,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int s_t[16];
   __shared__ float s_ss[16];
+  __shared__ float s_sx[16];
   __shared__ int s_last;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -328,12 +360,12 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
   if (nst > 1) gadvance<SPU>(P1, p.KQ);
   P2 = P1;
   if (nst > 2) gadvance<SPU>(P2, p.KQ);
-  BStage<NW, MAXCH> bs;
-  stage_b_issue<NW, MAXCH>(p, q * p.KQ * kSuperK, bs);
+  BStage<NW, MAXCH, NORM> bs;
+  stage_b_issue<NW, MAXCH, NORM>(p, q * p.KQ * kSuperK, bs);
   gload(s0, p, blk_base, P0, lw, le);
   gload(s1, p, blk_base, P1, lw, le);  // repeats stage 0 when nst == 1
   gload(s2, p, blk_base, P2, lw, le);
-  stage_b_finish<NW, MAXCH>(p, bs, ldsb, s_t, s_ss);
+  stage_b_finish<NW, MAXCH, NORM>(p, bs, ldsb, s_t, s_ss, s_sx);
   __syncthreads();
 
   if (ua < ub) {
@@ -434,9 +466,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) store_coherent(prs, dst + mat * 1024u, sum[mat]);
   }
-  if (p.x_scale && threadIdx.x < 16)
-    __hip_atomic_store(p.pss + (size_t)w * 16 + threadIdx.x, s_ss[threadIdx.x], __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  if ((p.x_scale || NORM) && threadIdx.x < 32)
+    __hip_atomic_store(p.pss + (size_t)w * 32 + threadIdx.x, threadIdx.x < 16 ? s_ss[threadIdx.x] : s_sx[threadIdx.x - 16],
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -450,13 +482,18 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 
   // last arrival: sum the S partials of every tile in K order and run the epilogue
   int th = 0;
-  if (p.x_scale) {
-    float ss = 0.f;
-    for (int qq = 0; qq < p.S; ++qq)
-      ss += __hip_atomic_load(p.pss + (size_t)(g * p.S + qq) * 16 + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float rs = 1.0f;
+  if (p.x_scale || NORM) {
+    float ss = 0.f, sx = 0.f;
+    for (int qq = 0; qq < p.S; ++qq) {
+      const float* ps = p.pss + (size_t)(g * p.S + qq) * 32;
+      ss += __hip_atomic_load(ps + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if constexpr (NORM) sx += __hip_atomic_load(ps + 16 + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if constexpr (NORM) rs = 1.0f / sqrtf(sx / (float)p.K + p.eps);
     const double gn = __longlong_as_double((long long)p.tg->max_row_norm_bits);
     const double un = __longlong_as_double((long long)p.tu->max_row_norm_bits);
-    const double bound = (double)ss * gn * un * (1.0 + 1.0 / 64.0);
+    const double bound = (double)ss * ((double)rs * rs) * gn * un * (1.0 + 1.0 / 64.0);
     int eb = 0;
     if (bound > 0.0) frexp(bound, &eb);
     th = bound > 0.0 ? 15 - eb : 0;
@@ -483,7 +520,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
           for (int mat = 0; mat < NMAT; ++mat) tot[mat] += v[qq][mat];
     }
-    gepilogue<WF, NMAT>(p, g * p.G + tl, tot, lane, th);
+    gepilogue<WF, NMAT>(p, g * p.G + tl, tot, lane, th, rs);
   }
 }
 
@@ -531,9 +568,9 @@ int plan_gemv(int rows, int K, int nmat, int num_cus, GemvPlan* out) {
   return 0;
 }
 
-template <int WF, int NMAT, int MAXCH>
+template <int WF, int NMAT, int MAXCH, bool NORM>
 static int launch_gemv_ch(const GvParams& p, size_t lds, hipStream_t s) {
-  auto kern = gemv_kernel<WF, NMAT, kGemvNW, MAXCH>;
+  auto kern = gemv_kernel<WF, NMAT, kGemvNW, MAXCH, NORM>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLds) != hipSuccess)
@@ -546,11 +583,11 @@ static int launch_gemv_ch(const GvParams& p, size_t lds, hipStream_t s) {
 
 // The staging register array is sized by a small set of buckets (loads beyond KQ are clamped
 // duplicates).
-template <int WF, int NMAT>
+template <int WF, int NMAT, bool NORM = false>
 static int launch_gemv(const GvParams& p, size_t lds, hipStream_t s) {
-  if (p.KQ <= 4) return launch_gemv_ch<WF, NMAT, 4>(p, lds, s);
-  if (p.KQ <= 10) return launch_gemv_ch<WF, NMAT, 10>(p, lds, s);
-  return launch_gemv_ch<WF, NMAT, kGemvMaxChunks>(p, lds, s);
+  if (p.KQ <= 4) return launch_gemv_ch<WF, NMAT, 4, NORM>(p, lds, s);
+  if (p.KQ <= 10) return launch_gemv_ch<WF, NMAT, 10, NORM>(p, lds, s);
+  return launch_gemv_ch<WF, NMAT, kGemvMaxChunks, NORM>(p, lds, s);
 }
 
 size_t gemv_max_slots(int rows, int K, int nmat) {
@@ -602,6 +639,8 @@ int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.P = pg.P;
   g.maxseg = pg.maxseg;
   g.x_scale = fmt == 1;
+  g.normw = (const uint16_t*)a.normw;
+  g.eps = a.eps;
   g.th_out = th;
   g.tg = (const Trailer*)(a.wg + trailer_offset(a.I, a.H, fmt));
   g.tu = (const Trailer*)(a.wu + trailer_offset(a.I, a.H, fmt));
@@ -609,7 +648,9 @@ int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.part = (float*)(a.ws + L.part_gu);
   g.pss = (float*)(a.ws + L.pss);
   g.counters = (int*)(a.ws + L.counters_gu);
-  int rc = fmt == 1 ? launch_gemv<1, 2>(g, gemv_lds_bytes(pg, 2), s) : launch_gemv<0, 2>(g, gemv_lds_bytes(pg, 2), s);
+  const size_t lg = gemv_lds_bytes(pg, 2);
+  int rc = a.normw ? (fmt == 1 ? launch_gemv<1, 2, true>(g, lg, s) : launch_gemv<0, 2, true>(g, lg, s))
+                   : (fmt == 1 ? launch_gemv<1, 2>(g, lg, s) : launch_gemv<0, 2>(g, lg, s));
   if (rc) return rc;
   profile_mark(2, s);
   GvParams d{};

@@ -55,7 +55,8 @@ struct WsLayout {
   size_t x16;                      // f16 [M, H] (bfp8 only)
   size_t h;                        // 16-bit [M, I]
   size_t part_gu, part_d;          // fp32 partial-sum slots
-  size_t pss;                      // per-workgroup token sums of squares (bfp8)
+  size_t pss;                      // per-workgroup token sums of squares
+  size_t xn;                       // bf16 [M, H] normalised activations (RMSNorm pass)
   size_t total;
 };
 WsLayout ws_layout(int M, int H, int I, int fmt);
@@ -71,9 +72,13 @@ struct ForwardArgs {
   uint8_t* ws;
   int M, H, I, fmt;
   int out_f32, res_f32;  // fp32 output / fp32 residual instead of bf16
+  const void* normw;     // RMSNorm prologue: bf16 [H] weight (gain 1 + w), or null
+  float eps;
 };
 // bfp8: x -> x16 = fp16(x * 2^tx[m]) and the h scale th[m], for all M tokens (qmlp_skinny.hip).
 int launch_prep(const ForwardArgs& a, hipStream_t s);
+// xn = bf16(rmsnorm(x) * (1 + w)) for M token rows (qmlp_skinny.hip).
+int launch_rmsnorm(const void* x, const void* w, float eps, int M, int H, void* xn, hipStream_t s);
 int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s);
 int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s);
 bool tiled_supported(int M, int H, int I);

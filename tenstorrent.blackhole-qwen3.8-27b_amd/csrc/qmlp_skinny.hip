@@ -463,6 +463,39 @@ static int launch_proj_m(const SkParams& p, hipStream_t s) {
   return p.M <= 16 ? launch_proj<WF, NMAT, 1>(p, s) : launch_proj<WF, NMAT, 2>(p, s);
 }
 
+// ---------------------------------------------------------------- RMSNorm pass (M > 16)
+//
+// xn = bf16(x * (1 / sqrt(mean(x^2) + eps)) * (1 + w)), one block per token row: the decoder's
+// ffn_norm (docker/qwen-c2-graft/graft/layer.py:110-112,228-237, add_unit_offset) as a separate
+// pass for the token counts whose kernels read the activations straight from memory.  The
+// row's sum of squares is reduced in a fixed order (deterministic).
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                      float eps, int H, uint16_t* __restrict__ xn) {
+  __shared__ float red[256];
+  const int m = blockIdx.x;
+  const uint16_t* xr = x + (size_t)m * H;
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < H; k += 256) {
+    const float v = bf16_to_f32(xr[k]);
+    ss = fmaf(v, v, ss);
+  }
+  red[threadIdx.x] = ss;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  const float rs = 1.0f / sqrtf(red[0] / (float)H + eps);
+  uint16_t* orow = xn + (size_t)m * H;
+  for (int k = threadIdx.x; k < H; k += 256) orow[k] = f32_to_bf16(bf16_to_f32(xr[k]) * rs * (1.0f + bf16_to_f32(w[k])));
+}
+
+int launch_rmsnorm(const void* x, const void* w, float eps, int M, int H, void* xn, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, s, (const uint16_t*)x, (const uint16_t*)w, eps, H,
+                     (uint16_t*)xn);
+  return check_launch("rmsnorm_kernel");
+}
+
 int launch_prep(const ForwardArgs& a, hipStream_t s) {
   const WsLayout L = ws_layout(a.M, a.H, a.I, a.fmt);
   const Trailer* tg = (const Trailer*)(a.wg + trailer_offset(a.I, a.H, 1));

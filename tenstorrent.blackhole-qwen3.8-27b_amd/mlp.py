@@ -278,6 +278,39 @@ def mlp_forward(x2d, weights, residual=None, out=None, workspace=None, stream=No
     return out
 
 
+def mlp_forward_rmsnorm(h2d, norm_weight, weights, eps=1e-6, out=None, workspace=None, stream=None,
+                        out_dtype=None):
+    """``out = h + down(silu(gate(n)) * up(n))`` with ``n = rmsnorm(h) * (1 + norm_weight)``: the
+    decoder's ``ffn_norm`` + MLP + residual add (``docker/qwen-c2-graft/graft/layer.py:352-357``)
+    in one call.  ``h2d`` bf16 ``[M, H]``; ``norm_weight`` bf16 ``[H]``; ``out`` may be ``h2d``."""
+    _check_device_tensor(h2d, "h", torch.bfloat16)
+    _check_device_tensor(norm_weight, "norm_weight", torch.bfloat16)
+    M, H = h2d.shape
+    I = weights.intermediate
+    if H != weights.hidden:
+        raise ValueError(f"h has hidden size {H}, weights expect {weights.hidden}")
+    if tuple(norm_weight.shape) != (H,):
+        raise ValueError(f"norm_weight must have shape ({H},)")
+    if out is None:
+        dt = torch.bfloat16 if out_dtype is None else out_dtype
+        if dt not in (torch.bfloat16, torch.float32):
+            raise ValueError("out_dtype must be bf16 or fp32")
+        out = torch.empty((M, H), dtype=dt, device=h2d.device)
+    else:
+        _check_device_tensor(out, "out")
+        if out.dtype not in (torch.bfloat16, torch.float32) or tuple(out.shape) != (M, H):
+            raise ValueError("out must be a bf16 or fp32 [M, H] tensor")
+    flags = _lib.OUT_F32 if out.dtype == torch.float32 else 0
+    if workspace is None:
+        workspace = new_workspace(M, H, I, weights.fmt, h2d.device, stream)
+    rc = _lib.lib().qmlp_forward_rmsnorm(_lib.ptr(h2d), _lib.ptr(norm_weight), float(eps), _lib.ptr(weights.w1.buf),
+                                         _lib.ptr(weights.w3.buf), _lib.ptr(weights.w2.buf), _lib.ptr(out),
+                                         _lib.ptr(workspace), workspace.numel(), M, H, I, weights.w1.fmt_code, flags,
+                                         _lib.stream_handle(stream))
+    _lib.check(rc, "qmlp_forward_rmsnorm")
+    return out
+
+
 class Qwen36MLP:
     """SwiGLU feed-forward network (``docker/qwen-c2-graft/graft/mlp.py:359-423``) on MI355X.
 
@@ -341,3 +374,25 @@ class Qwen36MLP:
         return y.reshape(shape) if out is None else out
 
     __call__ = forward
+
+    def forward_rmsnorm(self, h, norm_weight, eps=1e-6, out=None, out_dtype=None):
+        """``h + self.forward(rmsnorm(h) * (1 + norm_weight))`` in one call: the decoder's
+        ``ffn_norm`` -> MLP -> residual add (``layer.py:352-357``).  ``h`` ``[..., H]`` bf16;
+        ``out`` may be ``h`` itself."""
+        if not isinstance(h, torch.Tensor) or h.dtype != torch.bfloat16 or h.device.type != "cuda":
+            raise ValueError("h must be a bf16 GPU tensor")
+        if h.dim() < 1 or h.shape[-1] != self.weights.hidden:
+            raise ValueError(f"h must end in hidden size {self.weights.hidden}, got {tuple(h.shape)}")
+        shape = h.shape
+        h2d = h.reshape(-1, shape[-1])
+        if not h2d.is_contiguous():
+            h2d = h2d.contiguous()
+        M = h2d.shape[0]
+        o2d = None
+        if out is not None:
+            if tuple(out.shape) != tuple(shape):
+                raise ValueError("out must have h's shape")
+            o2d = out.reshape(M, shape[-1])
+        y = mlp_forward_rmsnorm(h2d, norm_weight, self.weights, eps=eps, out=o2d, workspace=self._workspace_for(M),
+                                out_dtype=out_dtype)
+        return y.reshape(shape) if out is None else out

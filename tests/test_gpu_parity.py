@@ -301,3 +301,50 @@ def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
     hw = _host_weights(pkg, sd, fmt)
     xf = x.float().cpu().numpy()
     _check(y32.cpu().numpy(), _oracle(xf, hw), f"prefill {fmt} H={H} I={I} M={M}")
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+def test_rmsnorm_prologue(pkg, cuda, fmt):
+    """h + MLP(rmsnorm(h) * (1 + w)) against the oracle's composition (the norm output rounded to
+    bf16 as the reference's separate norm produces it), across every dispatch width: fused into
+    the M <= 16 kernel, a separate pass for the others; then in place (out = h)."""
+    import torch
+    from qwen_mlp_amd import workloads
+
+    H, I = 1024, 3072
+    sd = workloads.state_dict(H, I, layer=9, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=200)
+    hw = _host_weights(pkg, sd, fmt)
+    g = torch.Generator(cuda).manual_seed(31)
+    nw = (torch.randn(H, generator=g, device=cuda) * 0.3).to(torch.bfloat16)
+    nwf = nw.float().cpu().numpy()
+    for M in (1, 5, 16, 24, 32, 64, 200):
+        h = (workloads.activations(M, H, seed=600 + M, device=cuda).float() * 7.0).to(torch.bfloat16)
+        y = mlp.forward_rmsnorm(h, nw, eps=1e-6, out_dtype=torch.float32)
+        y16 = mlp.forward_rmsnorm(h, nw, eps=1e-6)
+        torch.cuda.synchronize()
+        assert torch.equal(y.to(torch.bfloat16), y16)
+        hf = h.float().cpu().numpy()
+        ref = omlp.norm_swiglu(hf, nwf, hw["gate_proj"], hw["up_proj"], hw["down_proj"], 1e-6)
+        _check(y.cpu().numpy(), ref, f"rmsnorm {fmt} M={M}")
+        hh = h.clone()
+        mlp.forward_rmsnorm(hh, nw, eps=1e-6, out=hh)
+        torch.cuda.synchronize()
+        assert torch.equal(hh, y16)
+
+
+def test_rmsnorm_prologue_27b(pkg, cuda):
+    import torch
+    from qwen_mlp_amd import workloads
+
+    H, I, M = 5120, 17408, 16
+    sd = workloads.state_dict(H, I, layer=10, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format="bfp8", max_tokens=M)
+    nw = (torch.randn(H, generator=torch.Generator(cuda).manual_seed(5), device=cuda) * 0.3).to(torch.bfloat16)
+    h = (workloads.activations(M, H, seed=77, device=cuda).float() * 30.0).to(torch.bfloat16)
+    y = mlp.forward_rmsnorm(h, nw, eps=1e-6, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    hw = _host_weights(pkg, sd, "bfp8")
+    ref = omlp.norm_swiglu(h.float().cpu().numpy(), nw.float().cpu().numpy(), hw["gate_proj"], hw["up_proj"],
+                           hw["down_proj"], 1e-6)
+    _check(y.cpu().numpy(), ref, "rmsnorm 27B M=16 bfp8")

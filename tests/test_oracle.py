@@ -278,3 +278,50 @@ def test_tolerance_helper():
     assert ok and abs(err - 0.01) < 1e-12 and abs(bound - 1e-2 * math.sqrt((1 + 2.01**2) / 2)) < 1e-12
     ok, _, _ = omlp.tolerance_ok(np.array([1.0, 2.1]), np.array([1.0, 2.0]))
     assert not ok
+
+
+# ---------------------------------------------------------------- zero-centred RMSNorm prologue
+
+
+def test_rmsnorm_matches_torch_float64():
+    """Independent implementation: torch's rms_norm in float64 with weight 1 + w."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((6, 256)) * rng.uniform(0.01, 50, (6, 1))).astype(np.float32)
+    w = (rng.standard_normal(256) * 0.3).astype(np.float32)
+    for eps in (1e-6, 1e-2):
+        got = omlp.rmsnorm(x, w, eps)
+        ref = torch.nn.functional.rms_norm(torch.from_numpy(x).double(), (256,),
+                                           weight=1 + torch.from_numpy(w).double(), eps=eps).numpy()
+        assert np.max(np.abs(got - ref) / (np.abs(ref) + 1e-30)) < 2e-6
+
+
+def test_rmsnorm_closed_forms():
+    """With w = 0 every row's RMS is sqrt(ms / (ms + eps)); a constant row c maps to
+    c / sqrt(c^2 + eps); the unit offset matters (w = -1 gives zeros)."""
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((5, 512)).astype(np.float32)
+    eps = 1e-3
+    y = omlp.rmsnorm(x, np.zeros(512, np.float32), eps).astype(np.float64)
+    ms = np.mean(x.astype(np.float64) ** 2, axis=1)
+    assert np.allclose(np.sqrt(np.mean(y * y, axis=1)), np.sqrt(ms / (ms + eps)), rtol=1e-6)
+    c = np.full((1, 64), 0.25, np.float32)
+    assert np.allclose(omlp.rmsnorm(c, np.zeros(64, np.float32), eps), 0.25 / np.sqrt(0.0625 + eps), rtol=1e-6)
+    assert not np.any(omlp.rmsnorm(x, -np.ones(512, np.float32), eps))
+
+
+def test_norm_swiglu_composition():
+    """The fused feed-forward is the residual plus the MLP of the bf16-rounded norm output, and a
+    missing unit offset or a missing rounding would be visible."""
+    rng = np.random.default_rng(13)
+    H, I, M = 64, 96, 3
+    h = rng.standard_normal((M, H)).astype(np.float32) * 4
+    nw = (rng.standard_normal(H) * 0.2).astype(np.float32)
+    wg, wu, wd = (rng.standard_normal(s).astype(np.float32) * 0.1 for s in ((I, H), (I, H), (H, I)))
+    got = omlp.norm_swiglu(h, nw, wg, wu, wd, 1e-6)
+    from oracle import bf16 as obf16
+
+    n = obf16.round_f32(omlp.rmsnorm(h, nw, 1e-6))
+    assert np.array_equal(got, omlp.swiglu(n, wg, wu, wd, residual=h))
+    assert not np.allclose(got, omlp.swiglu(obf16.round_f32(omlp.rmsnorm(h, nw - 1, 1e-6)), wg, wu, wd, residual=h))
