@@ -79,12 +79,13 @@ __global__ void quantize_bfp8_kernel(const uint16_t* __restrict__ w, int rows, i
 
 // ---------------------------------------------------------------- packing
 
+// Writes the whole 256-byte trailer (zero padding), so a packed buffer's bytes depend only on the
+// weights -- packed buffers compare bit-for-bit and cache files are reproducible.
 __global__ void trailer_init_kernel(Trailer* t) {
-  if (threadIdx.x == 0) {
-    t->max_row_norm_bits = 0ull;
-    t->flushed_groups = 0u;
-    t->magic = kTrailerMagic;
-  }
+  uint32_t* words = (uint32_t*)t;
+  for (int i = threadIdx.x; i < kTrailer / 4; i += blockDim.x) words[i] = 0u;
+  __syncthreads();
+  if (threadIdx.x == 0) t->magic = kTrailerMagic;
 }
 
 // One workgroup (256 threads) per row: row base exponent, rowexp, L2 norm, flushed-group count.

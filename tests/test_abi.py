@@ -135,3 +135,30 @@ def test_skinny_split_covers_every_unit_once(pkg, rows, K, cus):
             assert max(owners) <= 2 and min(owners) >= 1
             if al:
                 assert max(owners) == 1
+
+
+def test_pack_checkpoint_finds_mlp_weights(tmp_path, pkg):
+    """The offline packer's checkpoint scan (CPU only): sharded index, key pattern, layer ranges."""
+    import json
+
+    import torch
+    from safetensors.torch import save_file
+
+    from qwen_mlp_amd import pack_checkpoint as pc
+
+    def t():
+        return torch.zeros((32, 256), dtype=torch.bfloat16)
+
+    save_file({"model.layers.0.mlp.gate_proj.weight": t(), "model.layers.0.mlp.up_proj.weight": t(),
+               "model.layers.0.self_attn.q_proj.weight": t()}, str(tmp_path / "a.safetensors"))
+    save_file({"model.layers.0.mlp.down_proj.weight": t(), "model.layers.3.mlp.gate_proj.weight": t()},
+              str(tmp_path / "b.safetensors"))
+    with open(tmp_path / "model.safetensors.index.json", "w") as f:
+        json.dump({"weight_map": {"x": "a.safetensors", "y": "b.safetensors"}}, f)
+    files = pc.checkpoint_files(str(tmp_path))
+    assert [p.split("/")[-1] for p in files] == ["a.safetensors", "b.safetensors"]
+    found = pc.mlp_keys(files)
+    assert sorted(found) == [0, 3] and sorted(found[0]) == ["down_proj", "gate_proj", "up_proj"]
+    assert pc.parse_layers("0", found) == [0] and pc.parse_layers(None, found) == [0, 3]
+    with pytest.raises(ValueError):
+        pc.parse_layers("0-2", found)

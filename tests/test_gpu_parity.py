@@ -348,3 +348,27 @@ def test_rmsnorm_prologue_27b(pkg, cuda):
     ref = omlp.norm_swiglu(h.float().cpu().numpy(), nw.float().cpu().numpy(), hw["gate_proj"], hw["up_proj"],
                            hw["down_proj"], 1e-6)
     _check(y.cpu().numpy(), ref, "rmsnorm 27B M=16 bfp8")
+
+
+def test_offline_packer_round_trip(pkg, cuda, tmp_path):
+    """HF safetensors -> pack_checkpoint -> cache files: the cached layer loads bit-identical to a
+    load-time conversion and the planar bfp8 files hold the canonical mantissas/exponents."""
+    import numpy as np
+    import torch
+    from safetensors.torch import save_file
+    from qwen_mlp_amd import pack_checkpoint, workloads
+
+    H, I = 1024, 3072
+    sds = [workloads.state_dict(H, I, layer=20 + i, device=cuda) for i in range(2)]
+    save_file({f"model.layers.{i}.mlp.{k}": v.cpu().contiguous() for i, sd in enumerate(sds) for k, v in sd.items()},
+              str(tmp_path / "model.safetensors"))
+    assert pack_checkpoint.main(["--checkpoint", str(tmp_path), "--out", str(tmp_path / "packed"), "--planar"]) == 0
+    for i, sd in enumerate(sds):
+        d = tmp_path / "packed" / f"layer_{i}"
+        cached = pkg.load_mlp_weights(cuda, {}, tensor_cache_path=str(d))  # nothing to convert
+        direct = pkg.load_mlp_weights(cuda, sd)
+        for f in ("w1", "w2", "w3"):
+            assert torch.equal(getattr(cached, f).buf, getattr(direct, f).buf)
+        q, e8 = pkg.quantize_bfp8(sd["gate_proj.weight"])
+        assert np.array_equal(np.load(d / "gate_proj.q.npy", mmap_mode="r"), q.cpu().numpy())
+        assert np.array_equal(np.load(d / "gate_proj.e8.npy", mmap_mode="r"), e8.cpu().numpy())
