@@ -372,3 +372,63 @@ def test_offline_packer_round_trip(pkg, cuda, tmp_path):
         q, e8 = pkg.quantize_bfp8(sd["gate_proj.weight"])
         assert np.array_equal(np.load(d / "gate_proj.q.npy", mmap_mode="r"), q.cpu().numpy())
         assert np.array_equal(np.load(d / "gate_proj.e8.npy", mmap_mode="r"), e8.cpu().numpy())
+
+
+def test_verify_arm_routes_decoder_mlps(pkg, cuda):
+    """A toy 2-layer decoder (norm -> MLP -> residual, layer.py:352-357, attention left out) whose
+    feed-forward modules are plain torch MLPs: inside the arm's scope the verify-width calls run the
+    library and match the torch path, other widths fall back, and the bindings come back."""
+    import torch
+    from qwen_mlp_amd import verify_arm, workloads
+
+    H, I = 1024, 3072
+
+    class TorchMLP:
+        def __init__(self, sd):
+            self.g, self.u, self.d = (sd[f"{k}.weight"].float() for k in ("gate_proj", "up_proj", "down_proj"))
+
+        def forward(self, x):
+            xf = x.float()
+            return ((torch.nn.functional.silu(xf @ self.g.T) * (xf @ self.u.T)) @ self.d.T).to(torch.bfloat16)
+
+    class ToyLayer:
+        def __init__(self, mlp):
+            self.feed_forward = mlp
+
+        def forward(self, h):
+            hf = h.float()
+            n = (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+            return (hf + self.feed_forward.forward(n).float()).to(torch.bfloat16)
+
+    sds = [workloads.state_dict(H, I, layer=30 + i, device=cuda) for i in range(2)]
+    layers = [ToyLayer(TorchMLP(sd)) for sd in sds]
+    amd = [pkg.Qwen36MLP(cuda, sd, weight_format="bf16", max_tokens=16) for sd in sds]
+    arm = verify_arm.VerifyArm([l.feed_forward for l in layers], amd, token_rows=16)
+
+    def run(h):
+        for layer in layers:
+            h = layer.forward(h)
+        return h
+
+    h16 = workloads.activations(16, H, seed=4, device=cuda).view(1, 1, 16, H)
+    h8 = workloads.activations(8, H, seed=5, device=cuda).view(1, 1, 8, H)
+    ref16, ref8 = run(h16), run(h8)
+    with arm.install():
+        out16, out8 = run(h16), run(h8)
+    torch.cuda.synchronize()
+    assert arm.audit == dict(rows=16, layers=2, hits=[1, 1], fallbacks=[1, 1], restored=True)
+    assert torch.equal(out8, ref8)  # fell back to the torch path
+    # The torch decoder rounds the MLP output to bf16 before the residual add, the library rounds
+    # the sum once: besides the 1e-2 * RMS bar allow two bf16 ulps of the reference per element.
+    y = out16.double().reshape(16, H).cpu().numpy()
+    r = ref16.double().reshape(16, H).cpu().numpy()
+    _, e = np.frexp(np.abs(r))
+    excess = float(np.max(np.abs(y - r) - 2 * np.ldexp(1.0, e - 8)))
+    bar = TOL * float(np.sqrt(np.mean(r * r)))
+    print(f"verify arm vs torch decoder: max(|err| - 2 ulp)={excess:.4e} bar={bar:.4e}", flush=True)
+    assert excess <= bar
+    assert all("forward" not in l.feed_forward.__dict__ for l in layers)
+    with pytest.raises(ZeroDivisionError):
+        with arm.install():
+            1 / 0
+    assert arm.audit["restored"] and not arm.active
