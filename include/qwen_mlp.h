@@ -159,12 +159,12 @@ int qmlp_set_profile_events(void* const* events, int n);
 
 /* ---------------------------------------------------------------- planning (host only)
  *
- * Work split of one weight-streaming projection: `rows` output rows (multiple of 16) over K
- * (multiple of 256) on `num_cus` compute units.  Fills out[0..3] = {workgroups, waves per
- * workgroup, units (16-row x 256-K blocks), tile-aligned (1) or stream-K (0)}.  Exposed so the
- * coverage of the split can be tested without a GPU, like the reference's worker-to-pair mapping
- * tests (scripts/ci/test_fused_1d.py:71-79). */
-int qmlp_plan_skinny(int rows, int K, int M, int num_cus, int* out4);
+ * Work split of the 16 < M <= 32 (stream-K) kernel for one projection: `rows` output rows
+ * (multiple of 16) over K (multiple of 256) on `num_cus` compute units.  Fills out[0..1] =
+ * {workgroups, tiles one wave may touch}.  Exposed so the coverage of the split can be tested
+ * without a GPU, like the reference's worker-to-pair mapping tests
+ * (scripts/ci/test_fused_1d.py:71-79). */
+int qmlp_plan_stream(int rows, int K, int num_cus, int* out2);
 
 /* Work split of the M <= 16 kernel for one projection with `nmat` matrices (2 = gate/up,
  * 1 = down): the (16-row tile x 256-K superblock) grid cut into tile groups x K splits.

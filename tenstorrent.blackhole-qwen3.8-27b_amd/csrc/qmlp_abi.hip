@@ -59,9 +59,8 @@ WsLayout ws_layout(int M, int H, int I, int fmt) {
   off = align256(off + (fmt == QMLP_FMT_BFP8 ? (size_t)M * H * 2 : 0));
   L.h = off;
   off = align256(off + (size_t)M * I * 2);
-  // partial-sum slots: the stream-K kernel (M > 16) needs 2 slots per workgroup of
-  // 2 matrices x 2 column tiles x 64 lanes x 16 B; the split kernel (M <= 16) one slot per
-  // (workgroup, tile) of NMAT x 64 lanes x 16 B.
+  // partial-sum slots: the stream-K kernel (M <= 32) needs 2 per workgroup of NMAT x 2 token
+  // groups x 64 lanes x 16 B, the split kernel (M <= 16) one per (workgroup, tile) of NMAT x 1 KB
   const size_t sk_gu = (size_t)2 * kMaxWorkgroups * (2 * 2 * 64 * 16);
   const size_t sk_d = (size_t)2 * kMaxWorkgroups * (1 * 2 * 64 * 16);
   const size_t gv_gu = gemv_max_slots(I, H, 2) * (2 * 64 * 16);
@@ -253,7 +252,7 @@ static int forward_impl(const char* fn, const void* x, const void* wg, const voi
   }
   if (stream_supported(M, H, I, di.num_cus)) return launch_forward_stream(a, di.num_cus, (hipStream_t)stream);
   if (tiled_supported(M, H, I)) return launch_forward_tiled(a, di.num_cus, (hipStream_t)stream);
-  return launch_forward_skinny(a, di.num_cus, (hipStream_t)stream);
+  return set_error(QMLP_E_SHAPE, "%s: no kernel for M=%d H=%d I=%d", fn, M, H, I);
 }
 
 int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* wd, const void* residual, void* out,
@@ -299,14 +298,12 @@ int qmlp_plan_split(int rows, int K, int nmat, int num_cus, int* out6) {
   return 0;
 }
 
-int qmlp_plan_skinny(int rows, int K, int M, int num_cus, int* out4) {
-  if (!out4) return set_error(QMLP_E_NULL, "qmlp_plan_skinny: null pointer");
-  SkinnyPlan p;
-  if (plan_skinny(rows, K, M, num_cus, &p)) return set_error(QMLP_E_SHAPE, "qmlp_plan_skinny: bad shape %dx%d", rows, K);
-  out4[0] = p.P;
-  out4[1] = p.NW;
-  out4[2] = p.T * p.C;
-  out4[3] = p.aligned;
+int qmlp_plan_stream(int rows, int K, int num_cus, int* out2) {
+  if (!out2) return set_error(QMLP_E_NULL, "qmlp_plan_stream: null pointer");
+  int P, maxseg;
+  if (plan_stream(rows, K, num_cus, &P, &maxseg)) return set_error(QMLP_E_SHAPE, "qmlp_plan_stream: bad shape %dx%d", rows, K);
+  out2[0] = P;
+  out2[1] = maxseg;
   return 0;
 }
 

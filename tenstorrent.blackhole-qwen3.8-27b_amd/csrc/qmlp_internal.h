@@ -21,17 +21,7 @@ int launch_unpack_bfp8(const void* packed, int rows, int cols, void* q, void* e8
 int launch_dequant(const void* packed, int rows, int cols, int fmt, float* out, hipStream_t s);
 int launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 
-// Work split of one weight-streaming projection.
-struct SkinnyPlan {
-  int P;        // workgroups
-  int NW;       // waves per workgroup
-  int T;        // 16-row tiles
-  int C;        // 256-K superblocks per tile
-  int aligned;  // workgroup ranges aligned to whole tiles (no cross-workgroup partial sums)
-};
 constexpr int kMaxWorkgroups = 512;  // upper bound used to size the workspace
-constexpr int kMaxSeg = 2;            // tiles one wave may touch
-int plan_skinny(int rows, int K, int M, int num_cus, SkinnyPlan* plan);
 
 // 2-D split of one projection for the M <= 16 weight-streaming kernel (qmlp_gemv.hip).
 struct GemvPlan {
@@ -75,11 +65,10 @@ struct ForwardArgs {
   const void* normw;     // RMSNorm prologue: bf16 [H] weight (gain 1 + w), or null
   float eps;
 };
-// bfp8: x -> x16 = fp16(x * 2^tx[m]) and the h scale th[m], for all M tokens (qmlp_skinny.hip).
+// bfp8: x -> x16 = fp16(x * 2^tx[m]) and the h scale th[m], for all M tokens (qmlp_prep.hip).
 int launch_prep(const ForwardArgs& a, hipStream_t s);
-// xn = bf16(rmsnorm(x) * (1 + w)) for M token rows (qmlp_skinny.hip).
+// xn = bf16(rmsnorm(x) * (1 + w)) for M token rows (qmlp_prep.hip).
 int launch_rmsnorm(const void* x, const void* w, float eps, int M, int H, void* xn, hipStream_t s);
-int launch_forward_skinny(const ForwardArgs& a, int num_cus, hipStream_t s);
 int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s);
 bool tiled_supported(int M, int H, int I);
 int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s);

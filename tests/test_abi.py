@@ -87,54 +87,78 @@ def test_python_wrapper_raises_value_error(pkg):
         _lib.check(-4, "x")
 
 
-def _plan(pkg, rows, K, cus):
-    out = (ctypes.c_int * 4)()
-    assert pkg.lib().qmlp_plan_skinny(rows, K, 16, cus, out) == 0
-    return list(out)
+SHAPES = [(17408, 5120), (5120, 17408), (3072, 1024), (1024, 3072), (8704, 5120), (5120, 8704), (256, 256),
+          (16, 256), (65536, 256), (512, 65536), (48, 768)]
+CUS = [256, 304, 80, 7, 1]
 
 
-def _simulate(P, NW, T, C, aligned, SPU):
-    """Python restatement of the kernel's range arithmetic."""
-    U = T * C
-    covered = [0] * U
-    tiles_of_wg = []
-    for w in range(P):
-        if aligned:
-            a, b = (w * T // P) * C, ((w + 1) * T // P) * C
-        else:
-            a, b = w * U // P, (w + 1) * U // P
-        tiles_of_wg.append(set(range(a // C, (b - 1) // C + 1)) if a < b else set())
-        for v in range(NW):
-            sa = a * SPU + v * (b - a) * SPU // NW
-            sb = a * SPU + (v + 1) * (b - a) * SPU // NW
-            if sa < sb:
-                spt = SPU * C
-                assert (sb - 1) // spt - sa // spt + 1 <= 2, "a wave may touch at most two tiles"
-            for st in range(sa, sb):
-                if st % SPU == 0:
-                    covered[st // SPU] += 1
-        # the kernel's closed form for the owner of a unit agrees with the ranges
-        for u in range(a, b):
-            owner = ((u // C + 1) * P - 1) // T if aligned else ((u + 1) * P - 1) // U
-            assert owner == w
-    return covered, tiles_of_wg
+def _wg_of_step(s, S, P):
+    """The stream-K kernel's closed form for the workgroup that owns step s."""
+    return ((s + 1) * P - 1) // S
 
 
-@pytest.mark.parametrize("rows,K,cus", [(17408, 5120, 256), (5120, 17408, 256), (3072, 1024, 256),
-                                        (1024, 3072, 256), (17408, 5120, 304), (8704, 5120, 256),
-                                        (5120, 8704, 256), (256, 256, 256), (16, 256, 256), (5120, 17408, 7)])
-def test_skinny_split_covers_every_unit_once(pkg, rows, K, cus):
-    P, NW, U, aligned = _plan(pkg, rows, K, cus)
-    T, C = rows // 16, K // 256
-    assert U == T * C and 1 <= P <= min(T, 512)
-    for SPU in (1, 2):
-        for al in (0, 1):
-            covered, tiles = _simulate(P, NW, T, C, al, SPU)
-            assert covered == [1] * U
-            owners = [sum(t in s for s in tiles) for t in range(T)]
-            assert max(owners) <= 2 and min(owners) >= 1
-            if al:
-                assert max(owners) == 1
+@pytest.mark.parametrize("rows,K", SHAPES)
+def test_stream_split_covers_every_step_once(pkg, rows, K):
+    """16 < M <= 32 kernel: the workgroup and wave step ranges tile [0, S) exactly, no wave touches
+    more tiles than the plan's LDS slots, the owner formula matches the ranges, and every tile
+    shared by workgroups is the first or last tile of each (its partial slot) -- the reference's
+    worker-to-pair coverage test (scripts/ci/test_fused_1d.py:71-79) for this split."""
+    for cus in CUS:
+        out = (ctypes.c_int * 2)()
+        assert pkg.lib().qmlp_plan_stream(rows, K, cus, out) == 0
+        P, maxseg = list(out)
+        T, SPT = rows // 16, (K // 256) * 4
+        S = T * SPT
+        assert 1 <= P <= min(S, 512) and maxseg <= 4
+        covered = [0] * S
+        share = {}
+        for w in range(P):
+            s0, s1 = w * S // P, (w + 1) * S // P
+            assert s1 > s0 and _wg_of_step(s0, S, P) == w and _wg_of_step(s1 - 1, S, P) == w
+            for v in range(8):
+                sa, sb = s0 + v * (s1 - s0) // 8, s0 + (v + 1) * (s1 - s0) // 8
+                for st in range(sa, sb):
+                    covered[st] += 1
+                if sb > sa:
+                    assert (sb - 1) // SPT - sa // SPT + 1 <= maxseg
+            for t in range(s0 // SPT, (s1 - 1) // SPT + 1):
+                share.setdefault(t, []).append(w)
+        assert covered == [1] * S
+        for t, ws in share.items():
+            assert ws == list(range(_wg_of_step(t * SPT, S, P), _wg_of_step((t + 1) * SPT - 1, S, P) + 1))
+            if len(ws) > 1:
+                for w in ws:
+                    assert t in ((w * S // P) // SPT, (((w + 1) * S // P) - 1) // SPT)
+
+
+@pytest.mark.parametrize("rows,K", SHAPES)
+@pytest.mark.parametrize("nmat", [1, 2])
+def test_gemv_split_covers_every_unit_once(pkg, rows, K, nmat):
+    """M <= 16 kernel: tile groups x K splits cover every (tile, superblock) unit once, each
+    workgroup's waves split its rectangle exactly, and no wave touches more than maxseg tiles."""
+    for cus in CUS:
+        out = (ctypes.c_int * 6)()
+        rc = pkg.lib().qmlp_plan_split(rows, K, nmat, cus, out)
+        if rc != 0:
+            continue  # no split fits (K too long for the staged activations): the caller falls back
+        P, G, S, KQ, Ng, maxseg = list(out)
+        T, C = rows // 16, K // 256
+        assert S * KQ == C and Ng == -(-T // G) and P == Ng * S and P <= max(cus, 1)
+        covered = [[0] * C for _ in range(T)]
+        for w in range(P):
+            g, q = w // S, w % S
+            Gw = min(G, T - g * G)
+            U = Gw * KQ
+            done = 0
+            for v in range(8):
+                ua, ub = v * U // 8, (v + 1) * U // 8
+                if ua < ub:
+                    assert (ub - 1) // KQ - ua // KQ + 1 <= maxseg
+                for u in range(ua, ub):
+                    covered[g * G + u // KQ][q * KQ + u % KQ] += 1
+                done += ub - ua
+            assert done == U
+        assert all(c == 1 for row in covered for c in row)
 
 
 def test_pack_checkpoint_finds_mlp_weights(tmp_path, pkg):
