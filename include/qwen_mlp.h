@@ -16,6 +16,9 @@
  *   QMLP_FMT_BFP8  bfp8 block float: 16 consecutive K values share one 8-bit exponent, each value
  *                  1 sign + 7 magnitude bits; dequantised in registers to fp16 matrix-core
  *                  operands, fp32 accumulation.
+ *   QMLP_FMT_BF4   bf4 block float: the same 16-value groups with 1 sign + 3 magnitude bits
+ *                  (0.5625 B/value).  In qmlp_forward it names the reference's mixed layout
+ *                  (mlp.py:17-19,164-169): gate_proj and up_proj packed bf4, down_proj packed bfp8.
  * Weights are used in the library's packed ("tiled") layout, produced once by qmlp_pack().
  * Matrices are row-major [out_features, in_features] like the HF checkpoint tensors
  * gate_proj.weight [I,H], up_proj.weight [I,H], down_proj.weight [H,I].
@@ -43,6 +46,7 @@ typedef struct ihipStream_t* qmlp_stream_t; /* == hipStream_t */
 
 #define QMLP_FMT_BF16 0
 #define QMLP_FMT_BFP8 1
+#define QMLP_FMT_BF4 2
 
 /* Message for the last failing call on this host thread ("" if none).  Host only. */
 const char* qmlp_last_error(void);
@@ -64,11 +68,18 @@ const char* qmlp_version(void);
 int qmlp_quantize_bfp8(const void* w_bf16, int rows, int cols, void* q, void* e8,
                        uint32_t* bad_groups, qmlp_stream_t stream);
 
+/* Canonical bf4 quantisation: as qmlp_quantize_bfp8 with magnitudes in [0, 7] (q in [-7, 7],
+ * scale 2^(e8-127) with e8 = exponent of the group maximum + 127 - 3).  Replaces the host
+ * quantiser inside ttnn.as_tensor(dtype=bfloat4_b) (mlp.py:17-19,164-169). */
+int qmlp_quantize_bf4(const void* w_bf16, int rows, int cols, void* q, void* e8,
+                      uint32_t* bad_groups, qmlp_stream_t stream);
+
 /* Bytes of the packed device buffer for one [rows, cols] matrix (host only, no GPU needed). */
 size_t qmlp_packed_bytes(int rows, int cols, int fmt);
 
 /* Pack one matrix into the library's tiled layout.
- *   fmt == QMLP_FMT_BFP8: src0 = q (int8 [rows,cols]), src1 = e8 (uint8 [rows,cols/16]).
+ *   fmt == QMLP_FMT_BFP8 or QMLP_FMT_BF4: src0 = q (int8 [rows,cols]), src1 = e8 (uint8
+ *   [rows,cols/16]) from the matching quantiser.
  *   fmt == QMLP_FMT_BF16: src0 = bf16 [rows,cols], src1 unused (may be null).
  * packed must hold qmlp_packed_bytes(rows, cols, fmt) bytes.  The trailer of the packed buffer
  * records the largest row L2 norm and the number of bfp8 groups too small to keep (see
@@ -88,6 +99,10 @@ int qmlp_packed_info(const void* packed, int rows, int cols, int fmt, double* ma
 int qmlp_unpack_bfp8(const void* packed, int rows, int cols, void* q, void* e8,
                      qmlp_stream_t stream);
 
+/* Inverse of qmlp_pack for bf4 (same contract as qmlp_unpack_bfp8). */
+int qmlp_unpack_bf4(const void* packed, int rows, int cols, void* q, void* e8,
+                    qmlp_stream_t stream);
+
 /* Dequantises a packed matrix to fp32 [rows, cols] with the same in-register routine the GEMM
  * kernels use.  Diagnostic/audit use. */
 int qmlp_dequant_packed(const void* packed, int rows, int cols, int fmt, float* out,
@@ -101,7 +116,8 @@ int qmlp_dequant_packed(const void* packed, int rows, int cols, int fmt, float* 
  * the residual add of Qwen36DecoderLayer.forward (layer.py:357) is fused when residual != null.
  *
  *   x        bf16 [M, H] row-major
- *   wg, wu   packed [I, H] (gate_proj, up_proj); wd packed [H, I] (down_proj); same fmt
+ *   wg, wu   packed [I, H] (gate_proj, up_proj); wd packed [H, I] (down_proj); all in fmt, except
+ *            that fmt == QMLP_FMT_BF4 takes wd packed QMLP_FMT_BFP8
  *   residual bf16 [M, H] or null
  *   out      bf16 [M, H]; may alias residual (each element is read before it is written by the
  *            same thread) but must not alias x

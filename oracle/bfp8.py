@@ -38,6 +38,15 @@ The GPU library re-encodes the canonical format losslessly for its kernels:
 
 Groups more than 19 binades below their row's largest group do not fit the half-precision window
 and are reported (``flushed``); the test data never produces one.
+
+bf4 (the reference's gate/up dtype)
+-----------------------------------
+The same canonical rule with 3 magnitude bits instead of 7 (``bf8_exact(values, 3)``): scale
+``2**(E - 3)`` (``e8 = E + 124``), ``q`` in ``[-7, 7]``.  Its device block (2304 bytes) holds the
+mantissas as 4-bit nibbles ``u = q + 8``: for K-step ``j`` of lane ``l`` the 16 values ``v0..v15``
+take 8 bytes at ``1024*(j // 2) + 16*l + 8*(j % 2)``; byte ``b`` of the first dword is
+``u_b | u_{b+4} << 4`` (``b = 0..3``), of the second ``u_{8+b} | u_{12+b} << 4``; then the same 256
+exponent bytes as bfp8 at offset 2048.
 """
 import numpy as np
 
@@ -48,7 +57,9 @@ TILE_ROWS = 16
 SUPER_K = 256
 STEPS = 4
 BLOCK_BYTES = STEPS * 1024 + 256
+BF4_BLOCK_BYTES = STEPS * 512 + 256
 BF16_BLOCK_BYTES = STEPS * 2048
+MANTISSA_BITS = {"bfp8": 7, "bf4": 3}
 TRAILER_BYTES = 256
 
 
@@ -57,8 +68,9 @@ def _check_shape(rows, cols):
         raise ValueError(f"rows must be a multiple of {TILE_ROWS} and cols of {SUPER_K}: {rows}x{cols}")
 
 
-def quantize(w_bits):
-    """Canonical bfp8 quantisation of a bf16 matrix given as uint16 words.
+def quantize(w_bits, mantissa_bits=7):
+    """Canonical block-float quantisation of a bf16 matrix given as uint16 words: bfp8 with 7
+    magnitude bits, bf4 with 3.
 
     Returns ``(q, e8)`` with ``q`` int8 ``[rows, cols]`` and ``e8`` uint8 ``[rows, cols // 16]``.
     Follows the shared-exponent rule of ``scripts/ci/ordered_cache_hw_plan.py:243-260``.
@@ -74,10 +86,11 @@ def quantize(w_bits):
     nonzero = v != 0
     shared = np.where(nonzero, ex, -100000).max(axis=2)
     zero_group = ~nonzero.any(axis=2)
-    e8 = np.clip(shared + 120, 1, 254)
+    qmax = 2 ** mantissa_bits - 1
+    e8 = np.clip(shared + 127 - mantissa_bits, 1, 254)
     e8 = np.where(zero_group, 0, e8)
     scale = np.ldexp(1.0, np.where(zero_group, 1, e8) - 127)
-    q = np.clip(np.rint(v / scale[..., None]), -127, 127)
+    q = np.clip(np.rint(v / scale[..., None]), -qmax, qmax)
     q = np.where(zero_group[..., None], 0, q)
     return q.astype(np.int8).reshape(rows, cols), e8.astype(np.uint8)
 
@@ -118,8 +131,61 @@ def row_base(e8):
 def packed_bytes(rows, cols, fmt):
     """Size of the device buffer for one matrix: tiles, then int32 rowexp, then a 256-byte trailer."""
     _check_shape(rows, cols)
-    block = BLOCK_BYTES if fmt == "bfp8" else BF16_BLOCK_BYTES
+    block = {"bfp8": BLOCK_BYTES, "bf4": BF4_BLOCK_BYTES, "bf16": BF16_BLOCK_BYTES}[fmt]
     return (rows // TILE_ROWS) * (cols // SUPER_K) * block + rows * 4 + TRAILER_BYTES
+
+
+def _device_exponents(e8):
+    """Per-group device exponent bytes ``E5 << 2``, the per-row base, and the flush count."""
+    base = row_base(e8)
+    e5 = e8.astype(np.int32) - base[:, None] + 20
+    live = e8 != 0
+    flushed = int((live & (e5 < 1)).sum())
+    return np.where(live & (e5 >= 1), e5 << 2, 0).astype(np.uint8), base, flushed
+
+
+def _exponent_block(dev_e, T, C):
+    # group index = 16*sb + 4*j + quarter -> lane-major dwords [T, C, quarter, row, step]
+    return dev_e.reshape(T, TILE_ROWS, C, STEPS, 4).transpose(0, 2, 4, 1, 3).reshape(T, C, 256)
+
+
+def pack_tiles_bf4(q, e8):
+    """bf4 device tile bytes + per-row exponent + flush count for canonical (q, e8), q in [-7, 7].
+
+    Returns ``(tiles uint8[T*C*2304], rowexp int32[rows], flushed int)``.
+    """
+    q = np.asarray(q, dtype=np.int8)
+    e8 = np.asarray(e8, dtype=np.uint8)
+    rows, cols = q.shape
+    _check_shape(rows, cols)
+    if np.abs(q.astype(np.int16)).max(initial=0) > 7:
+        raise ValueError("bf4 mantissas must lie in [-7, 7]")
+    T, C = rows // TILE_ROWS, cols // SUPER_K
+    dev_e, base, flushed = _device_exponents(e8)
+    u = (q.astype(np.int16) + 8).astype(np.uint8)
+    # [T, row, C, step, quarter, 16] -> [T, C, step, quarter, row, 16]
+    v = u.reshape(T, TILE_ROWS, C, STEPS, 4, GROUP).transpose(0, 2, 3, 4, 1, 5)
+    nib = np.concatenate([v[..., 0:4] | (v[..., 4:8] << 4), v[..., 8:12] | (v[..., 12:16] << 4)], axis=-1)
+    # [T, C, step, lane, 8] -> [T, C, pair, sub, lane, 8] -> [T, C, pair, lane, sub, 8]
+    nib = nib.reshape(T, C, 2, 2, 64, 8).transpose(0, 1, 2, 4, 3, 5).reshape(T, C, 2048)
+    tiles = np.concatenate([nib, _exponent_block(dev_e, T, C)], axis=2).reshape(-1)
+    return tiles, (base - 132).astype(np.int32), flushed
+
+
+def dequant_tiles_bf4(tiles, rowexp, rows, cols):
+    """Inverse of ``pack_tiles_bf4`` evaluated on the values: float32 ``[rows, cols]``."""
+    T, C = rows // TILE_ROWS, cols // SUPER_K
+    blk = np.asarray(tiles, dtype=np.uint8).reshape(T, C, BF4_BLOCK_BYTES)
+    nib = blk[:, :, :2048].reshape(T, C, 2, 64, 2, 8).transpose(0, 1, 2, 4, 3, 5).reshape(T, C, STEPS, 64, 8)
+    lo, hi = nib & 0x0F, nib >> 4
+    v = np.concatenate([lo[..., 0:4], hi[..., 0:4], lo[..., 4:8], hi[..., 4:8]], axis=-1)  # [T, C, step, lane, 16]
+    v = v.reshape(T, C, STEPS, 4, TILE_ROWS, GROUP).transpose(0, 4, 1, 2, 3, 5)
+    v = v.reshape(rows, cols // GROUP, GROUP).astype(np.float64) - 8.0
+    ex = blk[:, :, 2048:].reshape(T, C, 4, TILE_ROWS, STEPS).transpose(0, 3, 1, 4, 2)
+    e5 = ex.reshape(rows, cols // GROUP).astype(np.int64) >> 2
+    scale = np.where(e5 == 0, 0.0, np.ldexp(1.0, e5 - 15))
+    rs = np.ldexp(1.0, np.asarray(rowexp, dtype=np.int64))[:, None, None]
+    return (v * scale[..., None] * rs).reshape(rows, cols).astype(np.float32)
 
 
 def pack_tiles(q, e8):

@@ -28,8 +28,10 @@ uint16_t oracle_f32_to_bf16_rne(float f) {
   return (uint16_t)((w + bias) >> 16);
 }
 
-/* Returns the number of groups holding a non-finite value (their output is left zero). */
-int oracle_quantize_bfp8(const uint16_t* w, int rows, int cols, int8_t* q, uint8_t* e8) {
+/* Block-float quantiser with `mbits` magnitude bits (7: bfp8, 3: bf4).  Returns the number of
+ * groups holding a non-finite value (their output is left zero). */
+int oracle_quantize_bfp(const uint16_t* w, int rows, int cols, int8_t* q, uint8_t* e8, int mbits) {
+  const int qmax = (1 << mbits) - 1;
   int bad = 0;
   int groups = cols / 16;
   for (int r = 0; r < rows; ++r) {
@@ -59,20 +61,24 @@ int oracle_quantize_bfp8(const uint16_t* w, int rows, int cols, int8_t* q, uint8
         e8[(size_t)r * groups + g] = 0;
         continue;
       }
-      int e = shared + 120;
+      int e = shared + 127 - mbits;
       if (e < 1) e = 1;
       if (e > 254) e = 254;
       double scale = ldexp(1.0, e - 127);
       for (int i = 0; i < 16; ++i) {
         double t = nearbyint(v[i] / scale); /* default rounding mode: half to even */
-        if (t > 127.0) t = 127.0;
-        if (t < -127.0) t = -127.0;
+        if (t > qmax) t = qmax;
+        if (t < -qmax) t = -qmax;
         dq[i] = (int8_t)t;
       }
       e8[(size_t)r * groups + g] = (uint8_t)e;
     }
   }
   return bad;
+}
+
+int oracle_quantize_bfp8(const uint16_t* w, int rows, int cols, int8_t* q, uint8_t* e8) {
+  return oracle_quantize_bfp(w, rows, cols, q, e8, 7);
 }
 
 void oracle_dequantize_bfp8(const int8_t* q, const uint8_t* e8, int rows, int cols, float* out) {

@@ -25,6 +25,8 @@ def lib():
         i = ctypes.c_int
         _lib.oracle_quantize_bfp8.argtypes = [p, i, i, p, p]
         _lib.oracle_quantize_bfp8.restype = i
+        _lib.oracle_quantize_bfp.argtypes = [p, i, i, p, p, i]
+        _lib.oracle_quantize_bfp.restype = i
         _lib.oracle_dequantize_bfp8.argtypes = [p, p, i, i, p]
         _lib.oracle_swiglu_f32.argtypes = [p, p, p, p, p, p, p, i, i, i]
         _lib.oracle_f32_to_bf16_rne.argtypes = [ctypes.c_float]
@@ -36,12 +38,12 @@ def _ptr(a):
     return a.ctypes.data_as(ctypes.c_void_p)
 
 
-def quantize(w_bits):
+def quantize(w_bits, mantissa_bits=7):
     w_bits = np.ascontiguousarray(w_bits, dtype=np.uint16)
     rows, cols = w_bits.shape
     q = np.zeros((rows, cols), np.int8)
     e8 = np.zeros((rows, cols // 16), np.uint8)
-    bad = lib().oracle_quantize_bfp8(_ptr(w_bits), rows, cols, _ptr(q), _ptr(e8))
+    bad = lib().oracle_quantize_bfp(_ptr(w_bits), rows, cols, _ptr(q), _ptr(e8), mantissa_bits)
     if bad:
         raise ValueError(f"{bad} groups hold non-finite values")
     return q, e8

@@ -11,7 +11,8 @@ LIB_PATH = os.path.join(PKG_DIR, "libqwen_mlp.so")
 
 FMT_BF16 = 0
 FMT_BFP8 = 1
-FORMATS = {"bf16": FMT_BF16, "bfp8": FMT_BFP8}
+FMT_BF4 = 2
+FORMATS = {"bf16": FMT_BF16, "bfp8": FMT_BFP8, "bf4": FMT_BF4}
 
 QMLP_OK = 0
 OUT_F32 = 1
@@ -25,10 +26,12 @@ SIGNATURES = {
     "qmlp_last_error": (ctypes.c_char_p, []),
     "qmlp_version": (ctypes.c_char_p, []),
     "qmlp_quantize_bfp8": (_I, [_P, _I, _I, _P, _P, _U32P, _P]),
+    "qmlp_quantize_bf4": (_I, [_P, _I, _I, _P, _P, _U32P, _P]),
     "qmlp_packed_bytes": (_SZ, [_I, _I, _I]),
     "qmlp_pack": (_I, [_P, _P, _I, _I, _I, _P, _SZ, _P]),
     "qmlp_packed_info": (_I, [_P, _I, _I, _I, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_uint32), _P]),
     "qmlp_unpack_bfp8": (_I, [_P, _I, _I, _P, _P, _P]),
+    "qmlp_unpack_bf4": (_I, [_P, _I, _I, _P, _P, _P]),
     "qmlp_dequant_packed": (_I, [_P, _I, _I, _I, _P, _P]),
     "qmlp_forward": (_I, [_P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _P]),
     "qmlp_forward_ex": (_I, [_P, _P, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _P]),

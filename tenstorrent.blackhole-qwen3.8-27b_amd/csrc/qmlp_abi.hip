@@ -56,7 +56,7 @@ WsLayout ws_layout(int M, int H, int I, int fmt) {
   L.th = off;
   off = align256(off + (size_t)M * 4);
   L.x16 = off;
-  off = align256(off + (fmt == QMLP_FMT_BFP8 ? (size_t)M * H * 2 : 0));
+  off = align256(off + (fmt != QMLP_FMT_BF16 ? (size_t)M * H * 2 : 0));
   L.h = off;
   off = align256(off + (size_t)M * I * 2);
   // partial-sum slots: the stream-K kernel (M <= 32) needs 2 per workgroup of NMAT x 2 token
@@ -124,25 +124,37 @@ const char* qmlp_last_error(void) { return g_err; }
 
 const char* qmlp_version(void) { return "qwen_mlp 0.1 gfx950"; }
 
+static bool known_fmt(int fmt) { return fmt == QMLP_FMT_BF16 || fmt == QMLP_FMT_BFP8 || fmt == QMLP_FMT_BF4; }
+
 size_t qmlp_packed_bytes(int rows, int cols, int fmt) {
-  if (!shape_ok(rows, cols) || (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8)) return 0;
+  if (!shape_ok(rows, cols) || !known_fmt(fmt)) return 0;
   return packed_total(rows, cols, fmt);
+}
+
+static int quantize_impl(const char* fn, const void* w_bf16, int rows, int cols, void* q, void* e8,
+                         uint32_t* bad_groups, int mbits, qmlp_stream_t stream) {
+  if (!w_bf16 || !q || !e8) return set_error(QMLP_E_NULL, "%s: null pointer", fn);
+  if (rows <= 0 || cols <= 0 || cols % 16) return set_error(QMLP_E_SHAPE, "%s: bad shape %dx%d", fn, rows, cols);
+  if (!aligned16(w_bf16) || !aligned16(q)) return set_error(QMLP_E_ALIGN, "%s: misaligned pointer", fn);
+  DeviceInfo di;
+  if (int rc = current_device_info(&di)) return rc;
+  return launch_quantize(w_bf16, rows, cols, q, e8, bad_groups, mbits, (hipStream_t)stream);
 }
 
 int qmlp_quantize_bfp8(const void* w_bf16, int rows, int cols, void* q, void* e8, uint32_t* bad_groups,
                        qmlp_stream_t stream) {
-  if (!w_bf16 || !q || !e8) return set_error(QMLP_E_NULL, "qmlp_quantize_bfp8: null pointer");
-  if (rows <= 0 || cols <= 0 || cols % 16) return set_error(QMLP_E_SHAPE, "qmlp_quantize_bfp8: bad shape %dx%d", rows, cols);
-  if (!aligned16(w_bf16) || !aligned16(q)) return set_error(QMLP_E_ALIGN, "qmlp_quantize_bfp8: misaligned pointer");
-  DeviceInfo di;
-  if (int rc = current_device_info(&di)) return rc;
-  return launch_quantize(w_bf16, rows, cols, q, e8, bad_groups, (hipStream_t)stream);
+  return quantize_impl("qmlp_quantize_bfp8", w_bf16, rows, cols, q, e8, bad_groups, 7, stream);
+}
+
+int qmlp_quantize_bf4(const void* w_bf16, int rows, int cols, void* q, void* e8, uint32_t* bad_groups,
+                      qmlp_stream_t stream) {
+  return quantize_impl("qmlp_quantize_bf4", w_bf16, rows, cols, q, e8, bad_groups, 3, stream);
 }
 
 int qmlp_pack(const void* src0, const void* src1, int rows, int cols, int fmt, void* packed, size_t packed_bytes,
               qmlp_stream_t stream) {
-  if (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8) return set_error(QMLP_E_FORMAT, "qmlp_pack: unknown format %d", fmt);
-  if (!src0 || !packed || (fmt == QMLP_FMT_BFP8 && !src1)) return set_error(QMLP_E_NULL, "qmlp_pack: null pointer");
+  if (!known_fmt(fmt)) return set_error(QMLP_E_FORMAT, "qmlp_pack: unknown format %d", fmt);
+  if (!src0 || !packed || (fmt != QMLP_FMT_BF16 && !src1)) return set_error(QMLP_E_NULL, "qmlp_pack: null pointer");
   if (!shape_ok(rows, cols))
     return set_error(QMLP_E_SHAPE, "qmlp_pack: rows must be a multiple of 16 and cols of 256 (%dx%d)", rows, cols);
   if (!aligned16(src0) || !aligned16(packed)) return set_error(QMLP_E_ALIGN, "qmlp_pack: misaligned pointer");
@@ -157,8 +169,7 @@ int qmlp_pack(const void* src0, const void* src1, int rows, int cols, int fmt, v
 int qmlp_packed_info(const void* packed, int rows, int cols, int fmt, double* max_row_norm, uint32_t* flushed_groups,
                      qmlp_stream_t stream) {
   if (!packed) return set_error(QMLP_E_NULL, "qmlp_packed_info: null pointer");
-  if (!shape_ok(rows, cols) || (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8))
-    return set_error(QMLP_E_SHAPE, "qmlp_packed_info: bad shape/format");
+  if (!shape_ok(rows, cols) || !known_fmt(fmt)) return set_error(QMLP_E_SHAPE, "qmlp_packed_info: bad shape/format");
   DeviceInfo di;
   if (int rc = current_device_info(&di)) return rc;
   Trailer t;
@@ -174,18 +185,27 @@ int qmlp_packed_info(const void* packed, int rows, int cols, int fmt, double* ma
   return 0;
 }
 
-int qmlp_unpack_bfp8(const void* packed, int rows, int cols, void* q, void* e8, qmlp_stream_t stream) {
-  if (!packed || !q || !e8) return set_error(QMLP_E_NULL, "qmlp_unpack_bfp8: null pointer");
-  if (!shape_ok(rows, cols)) return set_error(QMLP_E_SHAPE, "qmlp_unpack_bfp8: bad shape %dx%d", rows, cols);
-  if (!aligned16(packed) || !aligned16(q)) return set_error(QMLP_E_ALIGN, "qmlp_unpack_bfp8: misaligned pointer");
+static int unpack_impl(const char* fn, const void* packed, int rows, int cols, int fmt, void* q, void* e8,
+                       qmlp_stream_t stream) {
+  if (!packed || !q || !e8) return set_error(QMLP_E_NULL, "%s: null pointer", fn);
+  if (!shape_ok(rows, cols)) return set_error(QMLP_E_SHAPE, "%s: bad shape %dx%d", fn, rows, cols);
+  if (!aligned16(packed) || !aligned16(q)) return set_error(QMLP_E_ALIGN, "%s: misaligned pointer", fn);
   DeviceInfo di;
   if (int rc = current_device_info(&di)) return rc;
-  return launch_unpack_bfp8(packed, rows, cols, q, e8, (hipStream_t)stream);
+  return launch_unpack(packed, rows, cols, fmt, q, e8, (hipStream_t)stream);
+}
+
+int qmlp_unpack_bfp8(const void* packed, int rows, int cols, void* q, void* e8, qmlp_stream_t stream) {
+  return unpack_impl("qmlp_unpack_bfp8", packed, rows, cols, QMLP_FMT_BFP8, q, e8, stream);
+}
+
+int qmlp_unpack_bf4(const void* packed, int rows, int cols, void* q, void* e8, qmlp_stream_t stream) {
+  return unpack_impl("qmlp_unpack_bf4", packed, rows, cols, QMLP_FMT_BF4, q, e8, stream);
 }
 
 int qmlp_dequant_packed(const void* packed, int rows, int cols, int fmt, float* out, qmlp_stream_t stream) {
   if (!packed || !out) return set_error(QMLP_E_NULL, "qmlp_dequant_packed: null pointer");
-  if (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8) return set_error(QMLP_E_FORMAT, "qmlp_dequant_packed: unknown format");
+  if (!known_fmt(fmt)) return set_error(QMLP_E_FORMAT, "qmlp_dequant_packed: unknown format");
   if (!shape_ok(rows, cols)) return set_error(QMLP_E_SHAPE, "qmlp_dequant_packed: bad shape %dx%d", rows, cols);
   if (!aligned16(packed) || !aligned16(out)) return set_error(QMLP_E_ALIGN, "qmlp_dequant_packed: misaligned pointer");
   DeviceInfo di;
@@ -194,8 +214,7 @@ int qmlp_dequant_packed(const void* packed, int rows, int cols, int fmt, float* 
 }
 
 size_t qmlp_workspace_bytes(int M, int H, int I, int fmt) {
-  if (M < 1 || M > 65536 || !shape_ok(16, H) || !shape_ok(16, I) || (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8))
-    return 0;
+  if (M < 1 || M > 65536 || !shape_ok(16, H) || !shape_ok(16, I) || !known_fmt(fmt)) return 0;
   return ws_layout(M, H, I, fmt).total;
 }
 
@@ -212,7 +231,7 @@ static int forward_impl(const char* fn, const void* x, const void* wg, const voi
                         const void* residual, void* out, void* ws, size_t ws_bytes, int M, int H, int I, int fmt,
                         int flags, const void* normw, float eps, qmlp_stream_t stream) {
   if (!x || !wg || !wu || !wd || !out || !ws) return set_error(QMLP_E_NULL, "%s: null pointer", fn);
-  if (fmt != QMLP_FMT_BF16 && fmt != QMLP_FMT_BFP8) return set_error(QMLP_E_FORMAT, "%s: unknown format %d", fn, fmt);
+  if (!known_fmt(fmt)) return set_error(QMLP_E_FORMAT, "%s: unknown format %d", fn, fmt);
   if (flags & ~(QMLP_OUT_F32 | QMLP_RESIDUAL_F32)) return set_error(QMLP_E_FORMAT, "%s: unknown flags 0x%x", fn, flags);
   if (M < 1 || M > 65536) return set_error(QMLP_E_SHAPE, "%s: M=%d out of range [1, 65536]", fn, M);
   if (!shape_ok(16, H) || !shape_ok(16, I))

@@ -9,6 +9,9 @@
 //     2^(E5-15) that scales that group (0 = all-zero group).
 //   * bf16 block (8192 B): per K-step two 1 KB halves; lane l owns values 0..7 of its 16 at
 //     j*2048 + 16l and values 8..15 at j*2048 + 1024 + 16l.
+//   * bf4 block (2304 B): 4-bit mantissas u = q + 8 (q in [-7, 7]); K-step j of lane l takes 8
+//     bytes at 1024*(j/2) + 16l + 8*(j%2): byte b of the first dword is u_b | u_{b+4} << 4, of the
+//     second u_{8+b} | u_{12+b} << 4; then the 256 exponent bytes as for bfp8, at 2048.
 //   * after the blocks: int32 rowexp[rows] (true weight = (u-128) * 2^(E5-15) * 2^rowexp), then a
 //     256-byte trailer {double max_row_norm; uint32 flushed_groups; uint32 magic}.
 // One 16x16x32 matrix-core product consumes, per lane, 8 consecutive K values of one weight row
@@ -24,6 +27,7 @@ constexpr int kTileRows = 16;
 constexpr int kSuperK = 256;
 constexpr int kSteps = 4;
 constexpr int kBfp8Block = kSteps * 1024 + 256;  // 4352
+constexpr int kBf4Block = kSteps * 512 + 256;     // 2304
 constexpr int kBf16Block = kSteps * 2048;        // 8192
 constexpr int kTrailer = 256;
 constexpr uint32_t kTrailerMagic = 0x514d4c50u;  // "PLMQ"
@@ -42,7 +46,8 @@ struct Trailer {
 };
 
 __host__ __device__ inline size_t tiles_bytes(int rows, int cols, int fmt) {
-  return (size_t)(rows / kTileRows) * (size_t)(cols / kSuperK) * (fmt == 1 ? kBfp8Block : kBf16Block);
+  return (size_t)(rows / kTileRows) * (size_t)(cols / kSuperK) *
+         (fmt == 1 ? kBfp8Block : (fmt == 2 ? kBf4Block : kBf16Block));
 }
 __host__ __device__ inline size_t rowexp_offset(int rows, int cols, int fmt) { return tiles_bytes(rows, cols, fmt); }
 __host__ __device__ inline size_t trailer_offset(int rows, int cols, int fmt) {
@@ -112,6 +117,52 @@ __device__ __forceinline__ void dq16(u32x4 w, f16x2 s, f16x8& a0, f16x8& a1) {
   dq4(w.w, s, c, p6, p7);
   a0 = f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
   a1 = f16x8{p4.x, p4.y, p5.x, p5.y, p6.x, p6.y, p7.x, p7.y};
+}
+
+// One lane's weights of one K-step, per format WF (0 bf16: two of these, 1 bfp8: 16 bytes,
+// 2 bf4: 8 bytes).
+template <int WF>
+struct StepWord {
+  typedef u32x4 type;
+};
+template <>
+struct StepWord<2> {
+  typedef u32x2 type;
+};
+
+// bf4: the lane's 16 nibbles of one K-step (two dwords) -> two f16x8 operands, exactly
+// ((1024 + u) * s - 1032 * s = (u - 8) * s).
+__device__ __forceinline__ void dq16_bf4(uint32_t d0, uint32_t d1, f16x2 s, f16x8& a0, f16x8& a1) {
+  const f16x2 c = s * f16x2{(_Float16)-1032.0f, (_Float16)-1032.0f};
+  f16x2 p0, p1, p2, p3, p4, p5, p6, p7;
+  dq4(d0 & 0x0f0f0f0fu, s, c, p0, p1);
+  dq4((d0 >> 4) & 0x0f0f0f0fu, s, c, p2, p3);
+  dq4(d1 & 0x0f0f0f0fu, s, c, p4, p5);
+  dq4((d1 >> 4) & 0x0f0f0f0fu, s, c, p6, p7);
+  a0 = f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+  a1 = f16x8{p4.x, p4.y, p5.x, p5.y, p6.x, p6.y, p7.x, p7.y};
+}
+
+// bf4 -> two bf16 x8 operands, exactly ((u - 8) * s has at most 4 significant bits).
+__device__ __forceinline__ void dq16_bf4_bf16(uint32_t d0, uint32_t d1, uint32_t ebyte, bf16x8& a0, bf16x8& a1) {
+  const float s = __uint_as_float(((ebyte >> 2) + 112u) << 23);
+  const float c = -8.0f * s;
+  uint32_t o[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t d = h ? d1 : d0;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {  // values 2b, 2b+1 (low nibbles) and 4+2b, 5+2b (high nibbles)
+      const float f0 = __builtin_fmaf((float)((d >> (16 * b)) & 0xfu), s, c);
+      const float f1 = __builtin_fmaf((float)((d >> (16 * b + 8)) & 0xfu), s, c);
+      const float f4 = __builtin_fmaf((float)((d >> (16 * b + 4)) & 0xfu), s, c);
+      const float f5 = __builtin_fmaf((float)((d >> (16 * b + 12)) & 0xfu), s, c);
+      o[4 * h + b] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+      o[4 * h + 2 + b] = __builtin_amdgcn_perm(__float_as_uint(f5), __float_as_uint(f4), 0x07060302u);
+    }
+  }
+  a0 = __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+  a1 = __builtin_bit_cast(bf16x8, u32x4{o[4], o[5], o[6], o[7]});
 }
 
 // The same 16 mantissas -> two bf16 x8 operands, exactly: (u - 128) * s has at most 8 significant

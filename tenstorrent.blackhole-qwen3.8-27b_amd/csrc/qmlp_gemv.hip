@@ -57,9 +57,10 @@ struct GvParams {
   int* counters;          // [Ng] arrival counters (left at zero)
 };
 
+// WF: 0 bf16, 1 bfp8, 2 bf4 weights.  A bf4 register holds two K-steps of the lane.
 template <int WF, int NMAT, int SPS>
 struct GStage {
-  u32x4 w[NMAT][SPS][WF ? 1 : 2];
+  u32x4 w[NMAT][WF == 2 ? SPS / 2 : SPS][WF ? 1 : 2];
   uint32_t e[NMAT];
 };
 
@@ -217,14 +218,14 @@ __device__ __forceinline__ void gadvance(GPos& q, int KQ) {
 template <int WF, int NMAT, int SPS>
 __device__ __forceinline__ void gload(GStage<WF, NMAT, SPS>& st, const GvParams& p, size_t blk_base, const GPos& q,
                                       uint32_t lw, uint32_t le) {
-  constexpr int BLK = WF ? kBfp8Block : kBf16Block;
+  constexpr int BLK = WF == 2 ? kBf4Block : (WF ? kBfp8Block : kBf16Block);
   const size_t blk = (blk_base + (size_t)q.tl * p.C + q.s) * BLK;
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
     const uint8_t* b = (mat ? p.w1 : p.w0) + blk;
-    const uint8_t* bp = b + q.part * SPS * (WF ? 1024 : 2048);
+    const uint8_t* bp = b + q.part * SPS * (WF == 2 ? 512 : (WF ? 1024 : 2048));
 #pragma unroll
-    for (int jj = 0; jj < SPS; ++jj) {
+    for (int jj = 0; jj < (WF == 2 ? SPS / 2 : SPS); ++jj) {
       if constexpr (WF) {
         st.w[mat][jj][0] = ld_stream((const u32x4*)(bp + lw + jj * 1024));
       } else {
@@ -249,7 +250,12 @@ __device__ __forceinline__ void gcompute(const GStage<WF, NMAT, SPS>& st, const 
     for (int mat = 0; mat < NMAT; ++mat) {
       if constexpr (WF) {
         f16x8 a0, a1;
-        dq16(st.w[mat][jj][0], scale_pair(st.e[mat], j), a0, a1);
+        if constexpr (WF == 2) {
+          const u32x4 d = st.w[mat][jj / 2][0];
+          dq16_bf4(jj & 1 ? d.z : d.x, jj & 1 ? d.w : d.y, scale_pair(st.e[mat], j), a0, a1);
+        } else {
+          dq16(st.w[mat][jj][0], scale_pair(st.e[mat], j), a0, a1);
+        }
         acc[mat][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(f16x8, b0), acc[mat][0], 0, 0, 0);
         acc[mat][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(f16x8, b1), acc[mat][1], 0, 0, 0);
       } else {
@@ -339,7 +345,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
   uint8_t* ldsb = lds;                                           // B operand
   f32x4* slots = (f32x4*)(lds + (size_t)p.KQ * kSteps * 64 * 32);  // [NW][maxseg][SLOT]
   const size_t blk_base = (size_t)(g * p.G) * p.C + (size_t)q * p.KQ;
-  const uint32_t lw = (uint32_t)lane * 16u, le = 4096u + (uint32_t)lane * 4u;
+  const uint32_t lw = (uint32_t)lane * 16u, le = (WF == 2 ? 2048u : 4096u) + (uint32_t)lane * 4u;
 
   // A wave without units still issues its prologue loads (of a valid unit) so that every load
   // before the staging barrier is unconditional.
@@ -638,7 +644,7 @@ int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.Ng = pg.Ng;
   g.P = pg.P;
   g.maxseg = pg.maxseg;
-  g.x_scale = fmt == 1;
+  g.x_scale = fmt != 0;
   g.normw = (const uint16_t*)a.normw;
   g.eps = a.eps;
   g.th_out = th;
@@ -649,13 +655,19 @@ int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.pss = (float*)(a.ws + L.pss);
   g.counters = (int*)(a.ws + L.counters_gu);
   const size_t lg = gemv_lds_bytes(pg, 2);
-  int rc = a.normw ? (fmt == 1 ? launch_gemv<1, 2, true>(g, lg, s) : launch_gemv<0, 2, true>(g, lg, s))
-                   : (fmt == 1 ? launch_gemv<1, 2>(g, lg, s) : launch_gemv<0, 2>(g, lg, s));
+  int rc;
+  if (fmt == 2)
+    rc = a.normw ? launch_gemv<2, 2, true>(g, lg, s) : launch_gemv<2, 2>(g, lg, s);
+  else if (fmt == 1)
+    rc = a.normw ? launch_gemv<1, 2, true>(g, lg, s) : launch_gemv<1, 2>(g, lg, s);
+  else
+    rc = a.normw ? launch_gemv<0, 2, true>(g, lg, s) : launch_gemv<0, 2>(g, lg, s);
   if (rc) return rc;
   profile_mark(2, s);
   GvParams d{};
   d.w0 = a.wd;
-  d.rowexp0 = (const int*)(a.wd + rowexp_offset(a.H, a.I, fmt));
+  const int dfmt = down_format(fmt);
+  d.rowexp0 = (const int*)(a.wd + rowexp_offset(a.H, a.I, dfmt));
   d.src = h;
   d.M = a.M;
   d.K = a.I;
@@ -676,7 +688,7 @@ int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.res_f32 = a.res_f32;
   d.part = (float*)(a.ws + L.part_d);
   d.counters = (int*)(a.ws + L.counters_d);
-  rc = fmt == 1 ? launch_gemv<1, 1>(d, gemv_lds_bytes(pd, 1), s) : launch_gemv<0, 1>(d, gemv_lds_bytes(pd, 1), s);
+  rc = dfmt == 1 ? launch_gemv<1, 1>(d, gemv_lds_bytes(pd, 1), s) : launch_gemv<0, 1>(d, gemv_lds_bytes(pd, 1), s);
   if (rc) return rc;
   profile_mark(3, s);
   return 0;

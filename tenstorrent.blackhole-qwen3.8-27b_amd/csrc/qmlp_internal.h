@@ -15,9 +15,9 @@ void set_profile_events(const hipEvent_t* ev);
 void profile_mark(int i, hipStream_t s);
 
 // Load-time kernels (qmlp_pack.hip).
-int launch_quantize(const void* w, int rows, int cols, void* q, void* e8, uint32_t* bad, hipStream_t s);
+int launch_quantize(const void* w, int rows, int cols, void* q, void* e8, uint32_t* bad, int mbits, hipStream_t s);
 int launch_pack(const void* src0, const void* src1, int rows, int cols, int fmt, void* packed, hipStream_t s);
-int launch_unpack_bfp8(const void* packed, int rows, int cols, void* q, void* e8, hipStream_t s);
+int launch_unpack(const void* packed, int rows, int cols, int fmt, void* q, void* e8, hipStream_t s);
 int launch_dequant(const void* packed, int rows, int cols, int fmt, float* out, hipStream_t s);
 int launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 
@@ -50,6 +50,9 @@ struct WsLayout {
   size_t total;
 };
 WsLayout ws_layout(int M, int H, int I, int fmt);
+
+// Format of down_proj for a forward in `fmt`: the bf4 layout pairs bf4 gate/up with bfp8 down.
+inline int down_format(int fmt) { return fmt == 2 ? 1 : fmt; }
 
 // Hot-path launchers.
 struct ForwardArgs {

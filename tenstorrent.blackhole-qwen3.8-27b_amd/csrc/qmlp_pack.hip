@@ -10,10 +10,11 @@ namespace qmlp {
 //
 // One thread per 16-value group.  Exact integer arithmetic on the bf16 words: a value is
 // sig * 2^ex0 with sig < 256; its frexp exponent is bitlen(sig) + ex0.  The shared exponent is the
-// largest of the group; q = round-half-even(sig * 2^(ex0 - (e8-127))) clamped to 127.
-__global__ void quantize_bfp8_kernel(const uint16_t* __restrict__ w, int rows, int cols,
-                                     int8_t* __restrict__ q, uint8_t* __restrict__ e8,
-                                     uint32_t* bad) {
+// largest of the group; q = round-half-even(sig * 2^(ex0 - (e8-127))) clamped to 2^MB - 1.
+// MB magnitude bits: 7 (bfp8) or 3 (bf4).
+template <int MB>
+__global__ void quantize_kernel(const uint16_t* __restrict__ w, int rows, int cols, int8_t* __restrict__ q,
+                                uint8_t* __restrict__ e8, uint32_t* bad) {
   const int groups = cols / 16;
   const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (long)rows * groups) return;
@@ -54,7 +55,7 @@ __global__ void quantize_bfp8_kernel(const uint16_t* __restrict__ w, int rows, i
   if (!finite) {
     if (bad) atomicAdd(bad, 1u);
   } else if (any) {
-    int e = shared + 120;
+    int e = shared + 127 - MB;
     e = e < 1 ? 1 : (e > 254 ? 254 : e);
     ebyte = (uint8_t)e;
 #pragma unroll
@@ -68,7 +69,7 @@ __global__ void quantize_bfp8_kernel(const uint16_t* __restrict__ w, int rows, i
         const int rem = sig[i] & ((1 << s) - 1), half = 1 << (s - 1);
         if (rem > half || (rem == half && (m & 1))) ++m;
       }
-      m = m > 127 ? 127 : m;
+      m = m > (1 << MB) - 1 ? (1 << MB) - 1 : m;
       const int qv = (v[i] & 0x8000) ? -m : m;
       out[i / 4] |= ((uint32_t)(qv & 0xff)) << (8 * (i % 4));
     }
@@ -155,6 +156,20 @@ __global__ void rowinfo_bf16_kernel(const uint16_t* __restrict__ w, int rows, in
   }
 }
 
+// Exponent dword of lane l of block (t, sb): byte j = E5 << 2 of the lane's group in K-step j.
+__device__ __forceinline__ uint32_t lane_exponents(const uint8_t* e8, int cols, int row, int sb, int qq,
+                                                   const int* rowexp) {
+  const int groups = cols / 16;
+  const int base = rowexp[row] + 132;
+  uint32_t dw = 0;
+  for (int jj = 0; jj < kSteps; ++jj) {
+    const int e = e8[(size_t)row * groups + sb * 16 + jj * 4 + qq];
+    const int e5 = e - base + 20;
+    dw |= ((e && e5 >= 1) ? (uint32_t)(e5 << 2) : 0u) << (8 * jj);
+  }
+  return dw;
+}
+
 // One thread per (block u, K-step j, lane l): 16 mantissa bytes; j == 0 threads also write the
 // lane's exponent dword.
 __global__ void pack_bfp8_kernel(const int8_t* __restrict__ q, const uint8_t* __restrict__ e8,
@@ -174,18 +189,102 @@ __global__ void pack_bfp8_kernel(const int8_t* __restrict__ q, const uint8_t* __
   const u32x4 src = *(const u32x4*)(q + (size_t)row * cols + k0);
   uint8_t* blk = packed + (size_t)u * kBfp8Block;
   *(u32x4*)(blk + j * 1024 + l * 16) = src ^ u32x4{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
-  if (j == 0) {
-    const int groups = cols / 16;
-    const int base = rowexp[row] + 132;
-    uint32_t dw = 0;
-    for (int jj = 0; jj < kSteps; ++jj) {
-      const int g = sb * 16 + jj * 4 + qq;
-      const int e = e8[(size_t)row * groups + g];
-      const int e5 = e - base + 20;
-      const uint32_t b = (e && e5 >= 1) ? (uint32_t)(e5 << 2) : 0u;
-      dw |= b << (8 * jj);
+  if (j == 0) *(uint32_t*)(blk + 4096 + l * 4) = lane_exponents(e8, cols, row, sb, qq, rowexp);
+}
+
+// bf4: one thread per (block u, K-step pair p, lane l): 2 x 16 mantissas -> 16 nibble bytes.
+__device__ __forceinline__ uint32_t nibbles8(const int8_t* v) {  // values v[0..7] -> one dword
+  uint32_t d = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    d |= ((uint32_t)(v[b] + 8) | ((uint32_t)(v[b + 4] + 8) << 4)) << (8 * b);
+  return d;
+}
+
+__global__ void pack_bf4_kernel(const int8_t* __restrict__ q, const uint8_t* __restrict__ e8, int rows, int cols,
+                                const int* __restrict__ rowexp, uint8_t* __restrict__ packed) {
+  const int C = cols / kSuperK;
+  const long tid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long total = (long)(rows / kTileRows) * C * 2 * 64;
+  if (tid >= total) return;
+  const int l = (int)(tid & 63);
+  const int pp = (int)((tid >> 6) & 1);
+  const long u = tid >> 7;
+  const int t = (int)(u / C), sb = (int)(u % C);
+  const int qq = l >> 4, row = t * kTileRows + (l & 15);
+  uint32_t out[4];
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int j = 2 * pp + sub;
+    int8_t v[16];
+    const int8_t* src = q + (size_t)row * cols + sb * kSuperK + j * 64 + qq * 16;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = src[i];
+    out[2 * sub] = nibbles8(v);
+    out[2 * sub + 1] = nibbles8(v + 8);
+  }
+  uint8_t* blk = packed + (size_t)u * kBf4Block;
+  *(u32x4*)(blk + pp * 1024 + l * 16) = u32x4{out[0], out[1], out[2], out[3]};
+  if (pp == 0) *(uint32_t*)(blk + 2048 + l * 4) = lane_exponents(e8, cols, row, sb, qq, rowexp);
+}
+
+// Inverse of pack_bf4_kernel (same thread mapping).
+__global__ void unpack_bf4_kernel(const uint8_t* __restrict__ packed, int rows, int cols,
+                                  const int* __restrict__ rowexp, int8_t* __restrict__ q, uint8_t* __restrict__ e8) {
+  const int C = cols / kSuperK;
+  const long tid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long total = (long)(rows / kTileRows) * C * 2 * 64;
+  if (tid >= total) return;
+  const int l = (int)(tid & 63);
+  const int pp = (int)((tid >> 6) & 1);
+  const long u = tid >> 7;
+  const int t = (int)(u / C), sb = (int)(u % C);
+  const int qq = l >> 4, row = t * kTileRows + (l & 15);
+  const uint8_t* blk = packed + (size_t)u * kBf4Block;
+  const u32x4 m = *(const u32x4*)(blk + pp * 1024 + l * 16);
+  const uint32_t dw = *(const uint32_t*)(blk + 2048 + l * 4);
+  const int base = rowexp[row] + 132;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int j = 2 * pp + sub;
+    int8_t* dst = q + (size_t)row * cols + sb * kSuperK + j * 64 + qq * 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t d = m[2 * sub + h];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        dst[8 * h + b] = (int8_t)((int)((d >> (8 * b)) & 0xfu) - 8);
+        dst[8 * h + b + 4] = (int8_t)((int)((d >> (8 * b + 4)) & 0xfu) - 8);
+      }
     }
-    *(uint32_t*)(blk + 4096 + l * 4) = dw;
+    const int e5 = (int)((dw >> (8 * j)) & 0xffu) >> 2;
+    e8[(size_t)row * (cols / 16) + sb * 16 + j * 4 + qq] = (uint8_t)(e5 ? e5 - 20 + base : 0);
+  }
+}
+
+// Audit dequantiser for bf4: the GEMM's dq16_bf4 routine, then the row scale.
+__global__ void dequant_bf4_kernel(const uint8_t* __restrict__ packed, int rows, int cols,
+                                   const int* __restrict__ rowexp, float* __restrict__ out) {
+  const int C = cols / kSuperK;
+  const long tid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long total = (long)(rows / kTileRows) * C * kSteps * 64;
+  if (tid >= total) return;
+  const int l = (int)(tid & 63);
+  const int j = (int)((tid >> 6) & 3);
+  const long u = tid >> 8;
+  const int t = (int)(u / C), sb = (int)(u % C);
+  const int row = t * kTileRows + (l & 15), qq = l >> 4;
+  const uint8_t* blk = packed + (size_t)u * kBf4Block;
+  const u32x2 m = *(const u32x2*)(blk + (j >> 1) * 1024 + l * 16 + (j & 1) * 8);
+  const uint32_t dw = *(const uint32_t*)(blk + 2048 + l * 4);
+  f16x8 a0, a1;
+  dq16_bf4(m.x, m.y, scale_pair(dw, j), a0, a1);
+  const int re = rowexp[row];
+  float* o = out + (size_t)row * cols + sb * kSuperK + j * 64 + qq * 16;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    o[i] = __builtin_amdgcn_ldexpf((float)a0[i], re);
+    o[8 + i] = __builtin_amdgcn_ldexpf((float)a1[i], re);
   }
 }
 
@@ -287,11 +386,15 @@ __global__ void fill_zero_kernel(u32x4* __restrict__ p, size_t n16) {
 
 static inline unsigned blocks_for(long n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
-int launch_quantize(const void* w, int rows, int cols, void* q, void* e8, uint32_t* bad, hipStream_t s) {
+int launch_quantize(const void* w, int rows, int cols, void* q, void* e8, uint32_t* bad, int mbits, hipStream_t s) {
   const long n = (long)rows * (cols / 16);
-  hipLaunchKernelGGL(quantize_bfp8_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s,
-                     (const uint16_t*)w, rows, cols, (int8_t*)q, (uint8_t*)e8, bad);
-  return check_launch("quantize_bfp8_kernel");
+  if (mbits == 3)
+    hipLaunchKernelGGL(quantize_kernel<3>, dim3(blocks_for(n, 256)), dim3(256), 0, s, (const uint16_t*)w, rows, cols,
+                       (int8_t*)q, (uint8_t*)e8, bad);
+  else
+    hipLaunchKernelGGL(quantize_kernel<7>, dim3(blocks_for(n, 256)), dim3(256), 0, s, (const uint16_t*)w, rows, cols,
+                       (int8_t*)q, (uint8_t*)e8, bad);
+  return check_launch("quantize_kernel");
 }
 
 int launch_pack(const void* src0, const void* src1, int rows, int cols, int fmt, void* packed, hipStream_t s) {
@@ -299,12 +402,18 @@ int launch_pack(const void* src0, const void* src1, int rows, int cols, int fmt,
   int* rowexp = (int*)(base + rowexp_offset(rows, cols, fmt));
   Trailer* tr = (Trailer*)(base + trailer_offset(rows, cols, fmt));
   hipLaunchKernelGGL(trailer_init_kernel, dim3(1), dim3(64), 0, s, tr);
-  if (fmt == 1) {
+  if (fmt == 1 || fmt == 2) {
     hipLaunchKernelGGL(rowinfo_bfp8_kernel, dim3(rows), dim3(256), 0, s, (const int8_t*)src0,
                        (const uint8_t*)src1, rows, cols, rowexp, tr);
-    const long n = (long)(rows / kTileRows) * (cols / kSuperK) * kSteps * 64;
-    hipLaunchKernelGGL(pack_bfp8_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, (const int8_t*)src0,
-                       (const uint8_t*)src1, rows, cols, (const int*)rowexp, base);
+    if (fmt == 1) {
+      const long n = (long)(rows / kTileRows) * (cols / kSuperK) * kSteps * 64;
+      hipLaunchKernelGGL(pack_bfp8_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, (const int8_t*)src0,
+                         (const uint8_t*)src1, rows, cols, (const int*)rowexp, base);
+    } else {
+      const long n = (long)(rows / kTileRows) * (cols / kSuperK) * 2 * 64;
+      hipLaunchKernelGGL(pack_bf4_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, (const int8_t*)src0,
+                         (const uint8_t*)src1, rows, cols, (const int*)rowexp, base);
+    }
   } else {
     hipLaunchKernelGGL(rowinfo_bf16_kernel, dim3(rows), dim3(256), 0, s, (const uint16_t*)src0, rows, cols,
                        rowexp, tr);
@@ -315,12 +424,19 @@ int launch_pack(const void* src0, const void* src1, int rows, int cols, int fmt,
   return check_launch("pack kernels");
 }
 
-int launch_unpack_bfp8(const void* packed, int rows, int cols, void* q, void* e8, hipStream_t s) {
+int launch_unpack(const void* packed, int rows, int cols, int fmt, void* q, void* e8, hipStream_t s) {
   const uint8_t* base = (const uint8_t*)packed;
-  const long n = (long)(rows / kTileRows) * (cols / kSuperK) * kSteps * 64;
-  hipLaunchKernelGGL(unpack_bfp8_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, base, rows, cols,
-                     (const int*)(base + rowexp_offset(rows, cols, 1)), (int8_t*)q, (uint8_t*)e8);
-  return check_launch("unpack_bfp8_kernel");
+  const int* rowexp = (const int*)(base + rowexp_offset(rows, cols, fmt));
+  if (fmt == 2) {
+    const long n = (long)(rows / kTileRows) * (cols / kSuperK) * 2 * 64;
+    hipLaunchKernelGGL(unpack_bf4_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, base, rows, cols, rowexp,
+                       (int8_t*)q, (uint8_t*)e8);
+  } else {
+    const long n = (long)(rows / kTileRows) * (cols / kSuperK) * kSteps * 64;
+    hipLaunchKernelGGL(unpack_bfp8_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, base, rows, cols, rowexp,
+                       (int8_t*)q, (uint8_t*)e8);
+  }
+  return check_launch("unpack kernel");
 }
 
 int launch_dequant(const void* packed, int rows, int cols, int fmt, float* out, hipStream_t s) {
@@ -329,6 +445,10 @@ int launch_dequant(const void* packed, int rows, int cols, int fmt, float* out, 
     const long n = (long)(rows / kTileRows) * (cols / kSuperK) * kSteps * 64;
     hipLaunchKernelGGL(dequant_bfp8_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, base, rows, cols,
                        (const int*)(base + rowexp_offset(rows, cols, 1)), out);
+  } else if (fmt == 2) {
+    const long n = (long)(rows / kTileRows) * (cols / kSuperK) * kSteps * 64;
+    hipLaunchKernelGGL(dequant_bf4_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, base, rows, cols,
+                       (const int*)(base + rowexp_offset(rows, cols, 2)), out);
   } else {
     const long n = (long)(rows / kTileRows) * (cols / kSuperK) * kSteps * 2 * 64;
     hipLaunchKernelGGL(dequant_bf16_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, s, base, rows, cols, out);

@@ -93,8 +93,8 @@ int launch_rmsnorm(const void* x, const void* w, float eps, int M, int H, void* 
 
 int launch_prep(const ForwardArgs& a, hipStream_t s) {
   const WsLayout L = ws_layout(a.M, a.H, a.I, a.fmt);
-  const Trailer* tg = (const Trailer*)(a.wg + trailer_offset(a.I, a.H, 1));
-  const Trailer* tu = (const Trailer*)(a.wu + trailer_offset(a.I, a.H, 1));
+  const Trailer* tg = (const Trailer*)(a.wg + trailer_offset(a.I, a.H, a.fmt));
+  const Trailer* tu = (const Trailer*)(a.wu + trailer_offset(a.I, a.H, a.fmt));
   hipLaunchKernelGGL(prep_kernel, dim3(a.M), dim3(256), 0, s, (const uint16_t*)a.x, a.H, tg, tu,
                      (uint16_t*)(a.ws + L.x16), (int*)(a.ws + L.tx), (int*)(a.ws + L.th));
   return check_launch("prep_kernel");

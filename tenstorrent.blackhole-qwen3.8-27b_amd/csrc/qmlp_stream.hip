@@ -53,7 +53,7 @@ struct StParams {
 
 template <int WF, int NMAT, int MG>
 struct SStage {
-  u32x4 w[NMAT][WF ? 1 : 2];
+  typename StepWord<WF>::type w[NMAT][WF ? 1 : 2];
   uint32_t e[NMAT];
   u32x4 b[MG][2];
 };
@@ -74,7 +74,7 @@ __device__ __forceinline__ int wg_of_step(int s, int S, int P) { return (int)(((
 
 template <int WF, int NMAT, int MG, int NW>
 __global__ __launch_bounds__(NW * 64) void stream_kernel(StParams p) {
-  constexpr int BLK = WF ? kBfp8Block : kBf16Block;
+  constexpr int BLK = WF == 2 ? kBf4Block : (WF ? kBfp8Block : kBf16Block);
   constexpr int SB = WF ? 1024 : 2048;
   constexpr int NACC = NMAT * MG;      // accumulated tiles per wave
   constexpr int CH = NACC >= 4 ? 1 : 2;  // independent product chains per tile
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(NW * 64) void stream_kernel(StParams p) {
   f32x4* slots = (f32x4*)lds;  // [NW][maxseg][NACC][64]
 
   // per-lane constant offsets
-  const uint32_t lw = (uint32_t)lane * 16u, le = 4096u + (uint32_t)lane * 4u;
+  const uint32_t lw = (uint32_t)lane * 16u, le = (WF == 2 ? 2048u : 4096u) + (uint32_t)lane * 4u;
   uint32_t boff[MG];  // byte offset of this lane's B row and quarter
 #pragma unroll
   for (int g = 0; g < MG; ++g) {
@@ -103,11 +103,11 @@ __global__ __launch_bounds__(NW * 64) void stream_kernel(StParams p) {
     const int sc = n > 0 ? min(st, sb - 1) : s0;
     const int tile = sc / SPT, ks = sc - tile * SPT;
     const size_t blk = ((size_t)tile * p.C + (ks >> 2)) * BLK;
-    const uint32_t wo = (uint32_t)(ks & 3) * SB;
+    const uint32_t wo = WF == 2 ? (uint32_t)(ks & 2) * 512u + (uint32_t)(ks & 1) * 8u : (uint32_t)(ks & 3) * SB;
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) {
       const uint8_t* b = (mat ? p.w1 : p.w0) + blk;
-      stg.w[mat][0] = ld_stream((const u32x4*)(b + wo + lw));
+      stg.w[mat][0] = ld_stream((const typename StepWord<WF>::type*)(b + wo + lw));
       if constexpr (WF) {
         stg.e[mat] = ld_stream((const uint32_t*)(b + le));
       } else {
@@ -148,7 +148,9 @@ __global__ __launch_bounds__(NW * 64) void stream_kernel(StParams p) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat) {
       bf16x8 a0, a1;
-      if constexpr (WF) {
+      if constexpr (WF == 2) {
+        dq16_bf4_bf16(stg.w[mat][0].x, stg.w[mat][0].y, (stg.e[mat] >> (8 * j)) & 0xffu, a0, a1);
+      } else if constexpr (WF) {
         dq16_bf16(stg.w[mat][0], (stg.e[mat] >> (8 * j)) & 0xffu, a0, a1);
       } else {
         a0 = __builtin_bit_cast(bf16x8, stg.w[mat][0]);
@@ -381,12 +383,13 @@ int launch_forward_stream(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.out = h;
   g.part = (float*)(a.ws + L.part_gu);
   g.counters = (int*)(a.ws + L.counters_gu);
-  int rc = fmt == 1 ? launch_stream_m<1, 2>(g, s) : launch_stream_m<0, 2>(g, s);
+  int rc = fmt == 2 ? launch_stream_m<2, 2>(g, s) : (fmt == 1 ? launch_stream_m<1, 2>(g, s) : launch_stream_m<0, 2>(g, s));
   if (rc) return rc;
   profile_mark(2, s);
   StParams d{};
   d.w0 = a.wd;
-  d.rowexp0 = (const int*)(a.wd + rowexp_offset(a.H, a.I, fmt));
+  const int dfmt = down_format(fmt);
+  d.rowexp0 = (const int*)(a.wd + rowexp_offset(a.H, a.I, dfmt));
   d.src = h;
   d.M = a.M;
   d.K = a.I;
@@ -402,7 +405,7 @@ int launch_forward_stream(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.res_f32 = a.res_f32;
   d.part = (float*)(a.ws + L.part_d);
   d.counters = (int*)(a.ws + L.counters_d);
-  rc = fmt == 1 ? launch_stream_m<1, 1>(d, s) : launch_stream_m<0, 1>(d, s);
+  rc = dfmt == 1 ? launch_stream_m<1, 1>(d, s) : launch_stream_m<0, 1>(d, s);
   if (rc) return rc;
   profile_mark(3, s);
   return 0;

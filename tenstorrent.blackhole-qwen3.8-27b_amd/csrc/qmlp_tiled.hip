@@ -44,7 +44,7 @@ struct TlParams {
 
 template <int WF, int NMAT, int TPW>
 struct TlStage {
-  u32x4 w[NMAT][TPW][WF ? 1 : 2];
+  typename StepWord<WF>::type w[NMAT][TPW][WF ? 1 : 2];
   uint32_t e[NMAT][TPW];
 };
 
@@ -54,8 +54,8 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   constexpr int SLOT = MG * 2048;      // LDS bytes of one 64-K step of B
   constexpr int CPT = MG * 128 / NT;   // 16-byte B chunks per thread per step
   static_assert(CPT * NT == MG * 128, "B chunks must divide evenly over the threads");
-  constexpr int BLK = WF ? kBfp8Block : kBf16Block;
-  constexpr int SB = WF ? 1024 : 2048;  // bytes of one K-step inside a weight block
+  constexpr int BLK = WF == 2 ? kBf4Block : (WF ? kBfp8Block : kBf16Block);
+  constexpr int SB = WF ? 1024 : 2048;  // bytes of one bf16/bfp8 K-step inside a weight block
   extern __shared__ __align__(16) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -92,18 +92,19 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
     for (int t = 0; t < TPW; ++t) wt[mat][t] = (mat ? p.w1 : p.w0) + (size_t)(tile0 + t) * p.C * BLK;
-  const uint32_t lw = (uint32_t)lane * 16u, le = 4096u + (uint32_t)lane * 4u;
+  const uint32_t lw = (uint32_t)lane * 16u, le = (WF == 2 ? 2048u : 4096u) + (uint32_t)lane * 4u;
   // Weights are re-read by every token block of the same features, so they are loaded with the
   // default cache policy (kept in L2 for the neighbouring blocks of the XCD).
   auto wload = [&](TlStage<WF, NMAT, TPW>& st, int step) {
     const int sc = min(step, nst - 1);
-    const uint32_t off = (uint32_t)(sc >> 2) * BLK + (uint32_t)(sc & 3) * SB;
+    const uint32_t off = (uint32_t)(sc >> 2) * BLK +
+                         (WF == 2 ? (uint32_t)(sc & 2) * 512u + (uint32_t)(sc & 1) * 8u : (uint32_t)(sc & 3) * SB);
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const uint8_t* b = wt[mat][t] + off;
-        st.w[mat][t][0] = *(const u32x4*)(b + lw);
+        st.w[mat][t][0] = *(const typename StepWord<WF>::type*)(b + lw);
         if constexpr (WF) {
           st.e[mat][t] = *(const uint32_t*)(wt[mat][t] + (uint32_t)(sc >> 2) * BLK + le);
         } else {
@@ -128,7 +129,13 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) dq16(st.w[mat][t][0], scale_pair(st.e[mat][t], step & 3), a[mat][t][0], a[mat][t][1]);
+        for (int t = 0; t < TPW; ++t) {
+          if constexpr (WF == 2)
+            dq16_bf4(st.w[mat][t][0].x, st.w[mat][t][0].y, scale_pair(st.e[mat][t], step & 3), a[mat][t][0],
+                     a[mat][t][1]);
+          else
+            dq16(st.w[mat][t][0], scale_pair(st.e[mat][t], step & 3), a[mat][t][0], a[mat][t][1]);
+        }
 #pragma unroll
       for (int g = 0; g < MG; ++g) {
         const f16x8 b0 = __builtin_bit_cast(f16x8, *(const u32x4*)(slot + g * 2048 + boff0));
@@ -282,7 +289,7 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   uint16_t* x16 = (uint16_t*)(a.ws + L.x16);
   uint16_t* h = (uint16_t*)(a.ws + L.h);
   profile_mark(0, s);
-  if (fmt == 1) {
+  if (fmt != 0) {
     int rc = launch_prep(a, s);
     if (rc) return rc;
   }
@@ -293,7 +300,7 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.w1 = a.wu;
   g.rowexp0 = (const int*)(a.wg + rowexp_offset(a.I, a.H, fmt));
   g.rowexp1 = (const int*)(a.wu + rowexp_offset(a.I, a.H, fmt));
-  g.src = fmt == 1 ? x16 : (const uint16_t*)a.x;
+  g.src = fmt != 0 ? x16 : (const uint16_t*)a.x;
   g.M = a.M;
   g.K = a.H;
   g.N = a.I;
@@ -302,12 +309,13 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.tsrc = tx;
   g.tout = th;
   g.out = h;
-  int rc = fmt == 1 ? launch_tiled<1, 2, 2>(g, s) : launch_tiled<0, 2, 2>(g, s);
+  int rc = fmt == 2 ? launch_tiled<2, 2, 2>(g, s) : (fmt == 1 ? launch_tiled<1, 2, 2>(g, s) : launch_tiled<0, 2, 2>(g, s));
   if (rc) return rc;
   profile_mark(2, s);
   TlParams d{};
   d.w0 = a.wd;
-  d.rowexp0 = (const int*)(a.wd + rowexp_offset(a.H, a.I, fmt));
+  const int dfmt = down_format(fmt);
+  d.rowexp0 = (const int*)(a.wd + rowexp_offset(a.H, a.I, dfmt));
   d.src = h;
   d.M = a.M;
   d.K = a.I;
@@ -319,7 +327,7 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.residual = a.residual;
   d.out_f32 = a.out_f32;
   d.res_f32 = a.res_f32;
-  rc = fmt == 1 ? launch_tiled<1, 1, 2>(d, s) : launch_tiled<0, 1, 2>(d, s);
+  rc = dfmt == 1 ? launch_tiled<1, 1, 2>(d, s) : launch_tiled<0, 1, 2>(d, s);
   if (rc) return rc;
   profile_mark(3, s);
   return 0;

@@ -22,7 +22,18 @@ import torch
 
 from . import _lib
 
-WEIGHT_FORMATS = ("bf16", "bfp8")
+# MLP weight formats.  "bf4" is the reference's mixed layout (``mlp.py:17-19,164-169``): gate/up in
+# bf4 (3 magnitude bits), down in bfp8.
+WEIGHT_FORMATS = ("bf16", "bfp8", "bf4")
+MATRIX_FORMATS = ("bf16", "bfp8", "bf4")
+_MANTISSA_BITS = {"bfp8": 7, "bf4": 3}
+
+
+def matrix_formats(fmt):
+    """(gate/up, down) matrix formats of an MLP weight format."""
+    if fmt not in WEIGHT_FORMATS:
+        raise ValueError(f"weight format must be one of {WEIGHT_FORMATS}, got {fmt!r}")
+    return (fmt, "bfp8") if fmt == "bf4" else (fmt, fmt)
 
 
 @dataclass
@@ -47,7 +58,7 @@ class PackedWeight:
     @property
     def stream_bytes(self):
         """Bytes of the weight values the forward pass streams (excludes row exponents/trailer)."""
-        per_value = 17 / 16 if self.fmt == "bfp8" else 2
+        per_value = {"bfp8": 17 / 16, "bf4": 9 / 16, "bf16": 2}[self.fmt]
         return int(self.rows * self.cols * per_value)
 
     def data_ptr(self):
@@ -67,6 +78,15 @@ def _check_device_tensor(t, name, dtype=None):
 
 def quantize_bfp8(w, stream=None):
     """Canonical bfp8 of a bf16 ``[rows, cols]`` GPU tensor -> ``(q int8 [rows, cols], e8 uint8 [rows, cols/16])``."""
+    return _quantize(w, "bfp8", stream)
+
+
+def quantize_bf4(w, stream=None):
+    """Canonical bf4 (q in [-7, 7]) of a bf16 ``[rows, cols]`` GPU tensor -> ``(q, e8)``."""
+    return _quantize(w, "bf4", stream)
+
+
+def _quantize(w, fmt, stream):
     _check_device_tensor(w, "w", torch.bfloat16)
     if w.dim() != 2:
         raise ValueError("w must be 2-D")
@@ -74,8 +94,9 @@ def quantize_bfp8(w, stream=None):
     q = torch.empty((rows, cols), dtype=torch.int8, device=w.device)
     e8 = torch.empty((rows, cols // 16), dtype=torch.uint8, device=w.device)
     bad = torch.zeros(1, dtype=torch.int32, device=w.device)
-    _lib.check(_lib.lib().qmlp_quantize_bfp8(_lib.ptr(w), rows, cols, _lib.ptr(q), _lib.ptr(e8), _lib.ptr(bad),
-                                             _lib.stream_handle(stream)), "qmlp_quantize_bfp8")
+    fn = "qmlp_quantize_" + fmt
+    _lib.check(getattr(_lib.lib(), fn)(_lib.ptr(w), rows, cols, _lib.ptr(q), _lib.ptr(e8), _lib.ptr(bad),
+                                       _lib.stream_handle(stream)), fn)
     if int(bad.item()):
         raise ValueError(f"weight holds non-finite values in {int(bad.item())} groups")
     return q, e8
@@ -93,33 +114,42 @@ def _read_info(pw, stream=None):
 
 def pack_canonical_bfp8(q, e8, strict=True, stream=None):
     """Pack canonical bfp8 (q int8 [rows, cols], e8 uint8 [rows, cols/16]) into the device layout."""
+    return pack_canonical(q, e8, "bfp8", strict, stream)
+
+
+def pack_canonical(q, e8, fmt="bfp8", strict=True, stream=None):
+    """Pack canonical block float (``fmt`` "bfp8" or "bf4") into the device layout."""
+    if fmt not in _MANTISSA_BITS:
+        raise ValueError(f"canonical format must be bfp8 or bf4, got {fmt!r}")
     _check_device_tensor(q, "q", torch.int8)
     _check_device_tensor(e8, "e8", torch.uint8)
     rows, cols = q.shape
     if tuple(e8.shape) != (rows, cols // 16):
         raise ValueError("e8 must be [rows, cols/16]")
-    nbytes = _lib.lib().qmlp_packed_bytes(rows, cols, _lib.FMT_BFP8)
+    code = _lib.FORMATS[fmt]
+    nbytes = _lib.lib().qmlp_packed_bytes(rows, cols, code)
     if nbytes == 0:
         raise ValueError(f"unsupported shape {rows}x{cols}: rows must be a multiple of 16 and cols of 256")
     buf = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
-    _lib.check(_lib.lib().qmlp_pack(_lib.ptr(q), _lib.ptr(e8), rows, cols, _lib.FMT_BFP8, _lib.ptr(buf), nbytes,
+    _lib.check(_lib.lib().qmlp_pack(_lib.ptr(q), _lib.ptr(e8), rows, cols, code, _lib.ptr(buf), nbytes,
                                     _lib.stream_handle(stream)), "qmlp_pack")
-    pw = _read_info(PackedWeight(buf, rows, cols, "bfp8"), stream)
+    pw = _read_info(PackedWeight(buf, rows, cols, fmt), stream)
     if strict and pw.flushed_groups:
-        raise ValueError(f"{pw.flushed_groups} bfp8 groups lie more than 19 binades below their row maximum")
+        raise ValueError(f"{pw.flushed_groups} {fmt} groups lie more than 19 binades below their row maximum")
     return pw
 
 
 def pack_weight(w, fmt="bfp8", strict=True, stream=None):
-    """bf16 ``[rows, cols]`` GPU tensor (HF layout: [out, in]) -> PackedWeight in ``fmt``."""
-    if fmt not in WEIGHT_FORMATS:
-        raise ValueError(f"weight format must be one of {WEIGHT_FORMATS}, got {fmt!r}")
+    """bf16 ``[rows, cols]`` GPU tensor (HF layout: [out, in]) -> PackedWeight in the matrix format
+    ``fmt`` ("bf16", "bfp8" or "bf4")."""
+    if fmt not in MATRIX_FORMATS:
+        raise ValueError(f"matrix format must be one of {MATRIX_FORMATS}, got {fmt!r}")
     _check_device_tensor(w, "w", torch.bfloat16)
     if w.dim() != 2:
         raise ValueError("w must be 2-D")
-    if fmt == "bfp8":
-        q, e8 = quantize_bfp8(w, stream)
-        return pack_canonical_bfp8(q, e8, strict=strict, stream=stream)
+    if fmt in _MANTISSA_BITS:
+        q, e8 = _quantize(w, fmt, stream)
+        return pack_canonical(q, e8, fmt, strict=strict, stream=stream)
     rows, cols = w.shape
     nbytes = _lib.lib().qmlp_packed_bytes(rows, cols, _lib.FMT_BF16)
     if nbytes == 0:
@@ -134,10 +164,18 @@ def unpack_bfp8(pw, stream=None):
     """Packed bfp8 -> canonical (q, e8) (lossless for unflushed groups)."""
     if pw.fmt != "bfp8":
         raise ValueError("unpack_bfp8 needs a bfp8 weight")
+    return unpack_canonical(pw, stream)
+
+
+def unpack_canonical(pw, stream=None):
+    """Packed bfp8 or bf4 -> canonical (q, e8) (lossless for unflushed groups)."""
+    if pw.fmt not in _MANTISSA_BITS:
+        raise ValueError("unpacking needs a bfp8 or bf4 weight")
     q = torch.empty((pw.rows, pw.cols), dtype=torch.int8, device=pw.buf.device)
     e8 = torch.empty((pw.rows, pw.cols // 16), dtype=torch.uint8, device=pw.buf.device)
-    _lib.check(_lib.lib().qmlp_unpack_bfp8(_lib.ptr(pw.buf), pw.rows, pw.cols, _lib.ptr(q), _lib.ptr(e8),
-                                           _lib.stream_handle(stream)), "qmlp_unpack_bfp8")
+    fn = "qmlp_unpack_" + pw.fmt
+    _lib.check(getattr(_lib.lib(), fn)(_lib.ptr(pw.buf), pw.rows, pw.cols, _lib.ptr(q), _lib.ptr(e8),
+                                       _lib.stream_handle(stream)), fn)
     return q, e8
 
 
@@ -182,6 +220,7 @@ class MLPWeights:
 
     @property
     def fmt(self):
+        """MLP weight format ("bf4" = bf4 gate/up with bfp8 down)."""
         return self.w1.fmt
 
     @property
@@ -198,19 +237,19 @@ def load_mlp_weights(device, state_dict, tensor_cache_path=None, args=None, weig
     may also come from ``args.mlp_weight_format``.
     """
     fmt = getattr(args, "mlp_weight_format", weight_format) if args is not None else weight_format
-    if fmt not in WEIGHT_FORMATS:
-        raise ValueError(f"weight format must be one of {WEIGHT_FORMATS}, got {fmt!r}")
+    gu_fmt, down_fmt = matrix_formats(fmt)
     device = torch.device(device) if not isinstance(device, torch.device) else device
     if device.type != "cuda":
         raise ValueError(f"device must be a GPU, got {device}")
     names = {"w1": "gate_proj", "w2": "down_proj", "w3": "up_proj"}
     packed = {}
     for field, name in names.items():
+        mfmt = down_fmt if field == "w2" else gu_fmt
         cache = None
         if tensor_cache_path is not None:
             from . import weight_cache
 
-            cache = weight_cache.cache_file(tensor_cache_path, name, fmt)
+            cache = weight_cache.cache_file(tensor_cache_path, name, mfmt)
             pw = weight_cache.load(cache, device) if os.path.exists(cache) else None
             if pw is not None:
                 packed[field] = pw
@@ -219,7 +258,7 @@ def load_mlp_weights(device, state_dict, tensor_cache_path=None, args=None, weig
         if not isinstance(w, torch.Tensor):
             w = torch.as_tensor(w)
         w = w.to(device=device, dtype=torch.bfloat16).contiguous()
-        packed[field] = pack_weight(w, fmt)
+        packed[field] = pack_weight(w, mfmt)
         del w
         if cache is not None:
             from . import weight_cache
@@ -229,9 +268,16 @@ def load_mlp_weights(device, state_dict, tensor_cache_path=None, args=None, weig
     I, H = weights.w1.rows, weights.w1.cols
     if (weights.w3.rows, weights.w3.cols) != (I, H) or (weights.w2.rows, weights.w2.cols) != (H, I):
         raise ValueError("gate/up must be [I, H] and down [H, I]")
-    if len({weights.w1.fmt, weights.w2.fmt, weights.w3.fmt}) != 1:
-        raise ValueError("all three weights must share one format")
+    check_formats(weights)
     return weights
+
+
+def check_formats(weights):
+    """The three matrices must form one MLP weight format (all alike, or bf4 gate/up + bfp8 down)."""
+    gu, down = matrix_formats(weights.w1.fmt) if weights.w1.fmt in WEIGHT_FORMATS else (None, None)
+    if weights.w3.fmt != gu or weights.w2.fmt != down:
+        raise ValueError(f"weight formats gate={weights.w1.fmt} up={weights.w3.fmt} down={weights.w2.fmt} do not form "
+                         f"one of {WEIGHT_FORMATS} (bf4 takes a bfp8 down_proj)")
 
 
 def mlp_forward(x2d, weights, residual=None, out=None, workspace=None, stream=None, out_dtype=None):

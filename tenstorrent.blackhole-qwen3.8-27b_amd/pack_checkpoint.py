@@ -8,7 +8,8 @@ conversion ahead of time for every layer:
 * ``<out>/layer_<i>/mlp.<name>.weight.<fmt>.qmlp`` -- the packed device layout with its header
   (``weight_cache``); ``load_mlp_weights(..., tensor_cache_path=<out>/layer_<i>)`` and
   ``Qwen36MLP(..., tensor_cache_path=...)`` memory-map it instead of quantising again;
-* with ``--planar`` (bfp8 only) also the canonical planar form, ``<name>.q.npy`` (int8
+  (``--format bf4`` writes gate/up as bf4 and down as bfp8, the reference's mixed layout);
+* with ``--planar`` (block-float formats) also the canonical planar form, ``<name>.q.npy`` (int8
   ``[rows, cols]`` signed mantissas) and ``<name>.e8.npy`` (uint8 ``[rows, cols/16]`` group
   exponents, scale ``2^(e8 - 127)``), plain ``.npy`` files that ``numpy.load(mmap_mode="r")`` maps.
 
@@ -18,7 +19,7 @@ bit-identical to what a load-time conversion produces.
 Usage (from the repository root)::
 
     python tenstorrent.blackhole-qwen3.8-27b_amd/pack_checkpoint.py --checkpoint DIR --out DIR
-        [--format bfp8|bf16] [--layers 0-63] [--planar]
+        [--format bfp8|bf4|bf16] [--layers 0-63] [--planar]
 """
 import argparse
 import glob
@@ -82,22 +83,24 @@ def pack_layer(entries, out_dir, fmt, device, planar=False):
 
     from . import mlp, weight_cache
 
+    gu_fmt, down_fmt = mlp.matrix_formats(fmt)
+    if planar and fmt == "bf16":
+        raise ValueError("--planar writes block-float mantissa/exponent planes (bfp8 or bf4)")
     written = []
     for name in ("gate_proj", "up_proj", "down_proj"):
+        mfmt = down_fmt if name == "down_proj" else gu_fmt
         if name not in entries:
             raise ValueError(f"missing {name}.weight")
         path, key = entries[name]
         with safe_open(path, framework="pt") as f:
             w = f.get_tensor(key)
         w = w.to(device=device, dtype=torch.bfloat16).contiguous()
-        pw = mlp.pack_weight(w, fmt)
-        cache = weight_cache.cache_file(out_dir, name, fmt)
+        pw = mlp.pack_weight(w, mfmt)
+        cache = weight_cache.cache_file(out_dir, name, mfmt)
         weight_cache.save(cache, pw)
         written.append(cache)
         if planar:
-            if fmt != "bfp8":
-                raise ValueError("--planar writes the bfp8 mantissa/exponent planes")
-            q, e8 = mlp.quantize_bfp8(w)
+            q, e8 = mlp.quantize_bf4(w) if mfmt == "bf4" else mlp.quantize_bfp8(w)
             np.save(os.path.join(out_dir, f"{name}.q.npy"), q.cpu().numpy())
             np.save(os.path.join(out_dir, f"{name}.e8.npy"), e8.cpu().numpy())
         del w, pw
@@ -108,9 +111,9 @@ def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--checkpoint", required=True, help="directory holding the HF *.safetensors files")
     ap.add_argument("--out", required=True, help="output directory (one layer_<i> subdirectory per layer)")
-    ap.add_argument("--format", default="bfp8", choices=("bfp8", "bf16"))
+    ap.add_argument("--format", default="bfp8", choices=("bfp8", "bf4", "bf16"))
     ap.add_argument("--layers", default=None, help="e.g. 0-63 or 0,5,7 (default: every layer found)")
-    ap.add_argument("--planar", action="store_true", help="also write the canonical bfp8 planes as .npy")
+    ap.add_argument("--planar", action="store_true", help="also write the canonical block-float planes as .npy")
     ap.add_argument("--device", default="cuda:0")
     args = ap.parse_args(argv)
     device = torch.device(args.device)

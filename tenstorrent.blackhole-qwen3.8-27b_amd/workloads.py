@@ -25,8 +25,12 @@ class Workload:
     gain: bool  # RMSNorm-like per-channel gain on the activations
 
     def weight_bytes(self):
-        per = 17 / 16 if self.fmt == "bfp8" else 2
-        return int(3 * self.hidden * self.intermediate * per)
+        """Bytes of the three matrices' values (gate/up and down per the weight format; "bf4"
+        pairs bf4 gate/up with a bfp8 down)."""
+        per = {"bfp8": 17 / 16, "bf4": 9 / 16, "bf16": 2}
+        gu = self.fmt
+        down = "bfp8" if self.fmt == "bf4" else self.fmt
+        return int(self.hidden * self.intermediate * (2 * per[gu] + per[down]))
 
     def algorithmic_bytes(self):
         """Weights streamed once + activation read + output write + residual read (bf16):
@@ -44,6 +48,10 @@ WORKLOADS = {
     "qwen3-27b-mlp-m1-bfp8": Workload("qwen3-27b-mlp-m1-bfp8", 5120, 17408, 1, "bfp8", True),
     "qwen3-27b-mlp-m32-bfp8": Workload("qwen3-27b-mlp-m32-bfp8", 5120, 17408, 32, "bfp8", True),
     "qwen3-27b-mlp-prefill-m2048-bfp8": Workload("qwen3-27b-mlp-prefill-m2048-bfp8", 5120, 17408, 2048, "bfp8", False),
+    "qwen3-27b-mlp-m16-bf4": Workload("qwen3-27b-mlp-m16-bf4", 5120, 17408, 16, "bf4", True),
+    "qwen3-27b-mlp-m1-bf4": Workload("qwen3-27b-mlp-m1-bf4", 5120, 17408, 1, "bf4", True),
+    "qwen3-27b-mlp-m32-bf4": Workload("qwen3-27b-mlp-m32-bf4", 5120, 17408, 32, "bf4", True),
+    "qwen3-27b-mlp-prefill-m2048-bf4": Workload("qwen3-27b-mlp-prefill-m2048-bf4", 5120, 17408, 2048, "bf4", False),
 }
 
 

@@ -37,15 +37,16 @@ def test_version_and_error_strings(pkg):
 
 
 @pytest.mark.parametrize("rows,cols", [(16, 256), (3072, 1024), (1024, 3072), (17408, 5120), (5120, 17408)])
-@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 def test_packed_bytes_matches_layout(pkg, rows, cols, fmt):
-    code = pkg.FMT_BFP8 if fmt == "bfp8" else pkg.FMT_BF16
+    code = {"bfp8": pkg.FMT_BFP8, "bf4": pkg.FMT_BF4, "bf16": pkg.FMT_BF16}[fmt]
     assert pkg.lib().qmlp_packed_bytes(rows, cols, code) == obfp8.packed_bytes(rows, cols, fmt)
 
 
 def test_packed_bytes_rejects_bad_shapes(pkg):
     lib = pkg.lib()
-    for rows, cols, fmt in ((15, 256, 1), (16, 255, 1), (0, 256, 0), (16, 256, 2), (-16, 256, 0)):
+    for rows, cols, fmt in ((15, 256, 1), (16, 255, 1), (0, 256, 0), (16, 256, 3), (16, 256, -1), (-16, 256, 0),
+                            (16, 128, 2)):
         assert lib.qmlp_packed_bytes(rows, cols, fmt) == 0
 
 
@@ -58,6 +59,8 @@ def test_workspace_bytes(pkg):
     assert lib.qmlp_workspace_bytes(0, 5120, 17408, 1) == 0
     assert lib.qmlp_workspace_bytes(16, 5000, 17408, 1) == 0
     assert lib.qmlp_workspace_bytes(2048, 5120, 17408, 1) > lib.qmlp_workspace_bytes(32, 5120, 17408, 1)
+    assert lib.qmlp_workspace_bytes(16, 5120, 17408, 2) == a  # bf4 stages the activations like bfp8
+    assert lib.qmlp_workspace_bytes(16, 5120, 17408, 3) == 0
 
 
 def test_forward_argument_errors_need_no_gpu(pkg):

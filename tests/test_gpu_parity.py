@@ -24,10 +24,12 @@ def _bits(t):
 def _host_weights(pkg, sd, fmt):
     """fp32 host copies of the identically dequantised weights (keyed by HF name)."""
     out = {}
+    gu_fmt, down_fmt = pkg.matrix_formats(fmt)
     for name in ("gate_proj", "up_proj", "down_proj"):
         w = sd[f"{name}.weight"]
-        if fmt == "bfp8":
-            q, e8 = pkg.quantize_bfp8(w)
+        mfmt = down_fmt if name == "down_proj" else gu_fmt
+        if mfmt in ("bfp8", "bf4"):
+            q, e8 = pkg.quantize_bf4(w) if mfmt == "bf4" else pkg.quantize_bfp8(w)
             out[name] = obfp8.dequantize(q.cpu().numpy(), e8.cpu().numpy())
         else:
             out[name] = obf16.bits_to_f32(_bits(w))
@@ -119,6 +121,42 @@ def test_pack_matches_oracle_layout(pkg, cuda, rows, cols):
     assert np.array_equal(pkg.dequantize(pb).cpu().numpy(), obf16.bits_to_f32(wb))
 
 
+@pytest.mark.parametrize("rows,cols", [(48, 768), (3072, 1024), (1024, 3072)])
+def test_bf4_pack_matches_oracle_layout(pkg, cuda, rows, cols):
+    """bf4: quantiser, packed bytes, row exponents, trailer, unpack and the kernels' dequant
+    routine all bit-exact against the oracle."""
+    import torch
+    from qwen_mlp_amd import workloads
+
+    w = workloads.weight(rows, cols, seed=3 * rows + cols, device=cuda)
+    # a few groups at the quantiser's edges: ties, a group maximum that rounds to 8 (clamped to
+    # 7), zero groups and groups far below the row maximum
+    w[0, :16] = torch.tensor([0.5625, -0.4375, 0.0625, 0.03125] * 4, dtype=torch.bfloat16, device=cuda)
+    w[1, :16] = 0.0
+    w[2, 16:32] = torch.full((16,), 0.96875, dtype=torch.bfloat16, device=cuda)  # 7.75 -> 8 -> 7
+    w[3, 32:48] *= 2.0 ** -12
+    wb = _bits(w)
+    q, e8 = pkg.quantize_bf4(w)
+    qo, eo = obfp8.quantize(wb, mantissa_bits=3)
+    assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(e8.cpu().numpy(), eo)
+    pw = pkg.pack_canonical(q, e8, "bf4")
+    tiles, rowexp, flushed = obfp8.pack_tiles_bf4(qo, eo)
+    buf = pw.buf.cpu().numpy()
+    assert buf.size == obfp8.packed_bytes(rows, cols, "bf4")
+    assert np.array_equal(buf[: tiles.size], tiles)
+    assert np.array_equal(buf[tiles.size: tiles.size + rows * 4].view(np.int32), rowexp)
+    assert pw.flushed_groups == flushed == 0
+    ref = obfp8.dequantize(qo, eo)
+    norms = obfp8.row_norms(ref)
+    assert abs(pw.max_row_norm - norms.max()) <= 1e-9 * norms.max()
+    qu, eu = pkg.unpack_canonical(pw)
+    assert np.array_equal(qu.cpu().numpy(), qo) and np.array_equal(eu.cpu().numpy(), eo)
+    d = pkg.dequantize(pw).cpu().numpy()
+    assert np.array_equal(d, ref) and np.array_equal(d, obfp8.dequant_tiles_bf4(tiles, rowexp, rows, cols))
+    # pack_weight takes the same route
+    assert torch.equal(pkg.pack_weight(w, "bf4").buf, pw.buf)
+
+
 def test_pack_reports_flushed_groups(pkg, cuda):
     import torch
 
@@ -139,7 +177,8 @@ def test_pack_reports_flushed_groups(pkg, cuda):
 
 
 @pytest.mark.parametrize("name", ["plumbing-h1024-i3072-m1-bf16", "qwen3-27b-mlp-m16-bf16", "qwen3-27b-mlp-m16-bfp8",
-                                  "qwen3-27b-mlp-m1-bfp8", "qwen3-27b-mlp-m32-bfp8"])
+                                  "qwen3-27b-mlp-m1-bfp8", "qwen3-27b-mlp-m32-bfp8", "qwen3-27b-mlp-m16-bf4",
+                                  "qwen3-27b-mlp-m1-bf4", "qwen3-27b-mlp-m32-bf4"])
 def test_forward_workloads(pkg, cuda, name):
     import torch
     from qwen_mlp_amd import workloads
@@ -166,7 +205,7 @@ def test_forward_workloads(pkg, cuda, name):
     _check_bf16(y16.reshape(wl.tokens, wl.hidden).float().cpu().numpy(), ref, name)
 
 
-@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 def test_forward_every_small_width(pkg, cuda, fmt):
     import torch
     from qwen_mlp_amd import workloads
@@ -183,7 +222,7 @@ def test_forward_every_small_width(pkg, cuda, fmt):
         _check(y.cpu().numpy(), _oracle(xf, hw), f"{fmt} H={H} I={I} M={M}")
 
 
-@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 def test_zero_input_and_aliasing(pkg, cuda, fmt):
     import torch
     from qwen_mlp_amd import workloads
@@ -203,7 +242,7 @@ def test_zero_input_and_aliasing(pkg, cuda, fmt):
     assert torch.equal(rr, expect)
 
 
-@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 def test_bitwise_deterministic(pkg, cuda, fmt):
     import torch
     from qwen_mlp_amd import workloads
@@ -219,7 +258,7 @@ def test_bitwise_deterministic(pkg, cuda, fmt):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 def test_graph_capture_replays(pkg, cuda, fmt):
     import torch
     from qwen_mlp_amd import workloads
@@ -282,7 +321,7 @@ def test_shape_errors(pkg, cuda):
         pkg.pack_weight(torch.zeros((17, 256), dtype=torch.bfloat16, device=cuda))
 
 
-@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 @pytest.mark.parametrize("H,I,M", [(1024, 3072, 2048), (5120, 17408, 256), (1024, 3072, 200)])
 def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
     """Many-token forwards (the LDS-tiled matrix-core kernels): a full 2048-token chunk, the 27B
@@ -303,7 +342,7 @@ def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
     _check(y32.cpu().numpy(), _oracle(xf, hw), f"prefill {fmt} H={H} I={I} M={M}")
 
 
-@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 def test_rmsnorm_prologue(pkg, cuda, fmt):
     """h + MLP(rmsnorm(h) * (1 + w)) against the oracle's composition (the norm output rounded to
     bf16 as the reference's separate norm produces it), across every dispatch width: fused into
@@ -350,9 +389,10 @@ def test_rmsnorm_prologue_27b(pkg, cuda):
     _check(y.cpu().numpy(), ref, "rmsnorm 27B M=16 bfp8")
 
 
-def test_offline_packer_round_trip(pkg, cuda, tmp_path):
+@pytest.mark.parametrize("fmt", ["bfp8", "bf4"])
+def test_offline_packer_round_trip(pkg, cuda, tmp_path, fmt):
     """HF safetensors -> pack_checkpoint -> cache files: the cached layer loads bit-identical to a
-    load-time conversion and the planar bfp8 files hold the canonical mantissas/exponents."""
+    load-time conversion and the planar files hold the canonical mantissas/exponents."""
     import numpy as np
     import torch
     from safetensors.torch import save_file
@@ -362,16 +402,21 @@ def test_offline_packer_round_trip(pkg, cuda, tmp_path):
     sds = [workloads.state_dict(H, I, layer=20 + i, device=cuda) for i in range(2)]
     save_file({f"model.layers.{i}.mlp.{k}": v.cpu().contiguous() for i, sd in enumerate(sds) for k, v in sd.items()},
               str(tmp_path / "model.safetensors"))
-    assert pack_checkpoint.main(["--checkpoint", str(tmp_path), "--out", str(tmp_path / "packed"), "--planar"]) == 0
+    assert pack_checkpoint.main(["--checkpoint", str(tmp_path), "--out", str(tmp_path / "packed"), "--planar",
+                                 "--format", fmt]) == 0
+    quant = pkg.quantize_bf4 if fmt == "bf4" else pkg.quantize_bfp8
     for i, sd in enumerate(sds):
         d = tmp_path / "packed" / f"layer_{i}"
-        cached = pkg.load_mlp_weights(cuda, {}, tensor_cache_path=str(d))  # nothing to convert
-        direct = pkg.load_mlp_weights(cuda, sd)
+        cached = pkg.load_mlp_weights(cuda, {}, tensor_cache_path=str(d), weight_format=fmt)  # nothing to convert
+        direct = pkg.load_mlp_weights(cuda, sd, weight_format=fmt)
+        assert (cached.w1.fmt, cached.w2.fmt, cached.w3.fmt) == (fmt, "bfp8", fmt)
         for f in ("w1", "w2", "w3"):
             assert torch.equal(getattr(cached, f).buf, getattr(direct, f).buf)
-        q, e8 = pkg.quantize_bfp8(sd["gate_proj.weight"])
+        q, e8 = quant(sd["gate_proj.weight"])
         assert np.array_equal(np.load(d / "gate_proj.q.npy", mmap_mode="r"), q.cpu().numpy())
         assert np.array_equal(np.load(d / "gate_proj.e8.npy", mmap_mode="r"), e8.cpu().numpy())
+        q, e8 = pkg.quantize_bfp8(sd["down_proj.weight"])
+        assert np.array_equal(np.load(d / "down_proj.q.npy", mmap_mode="r"), q.cpu().numpy())
 
 
 def test_verify_arm_routes_decoder_mlps(pkg, cuda):

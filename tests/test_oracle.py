@@ -325,3 +325,60 @@ def test_norm_swiglu_composition():
     n = obf16.round_f32(omlp.rmsnorm(h, nw, 1e-6))
     assert np.array_equal(got, omlp.swiglu(n, wg, wu, wd, residual=h))
     assert not np.allclose(got, omlp.swiglu(obf16.round_f32(omlp.rmsnorm(h, nw - 1, 1e-6)), wg, wu, wd, residual=h))
+
+
+# ---------------------------------------------------------------- bf4 (3 magnitude bits)
+
+
+def test_bf4_round_trip_exact_on_representable_groups():
+    """Groups that the reference's predicate with 3 mantissa bits accepts quantise exactly."""
+    rng = np.random.RandomState(41)
+    groups = 4096
+    q = rng.randint(-7, 8, size=(groups, 16))
+    q[:, 0] = np.where(rng.rand(groups) < 0.5, 1, -1) * rng.randint(4, 8, size=groups)  # max |q| in [4, 7]
+    E = rng.randint(-40, 40, size=groups)
+    v = (q * np.ldexp(1.0, (E - 3))[:, None]).astype(np.float32)
+    words = bf16.f32_to_bits(v)
+    assert bfp8.bf8_exact(v, mantissa_bits=3) and not bfp8.bf8_exact(v * 1.0625, mantissa_bits=3)
+    qq, e8 = bfp8.quantize(words.reshape(groups // 4, 64), mantissa_bits=3)
+    assert np.array_equal(qq.reshape(groups, 16), q)
+    assert np.array_equal(e8.reshape(groups), (E + 124).astype(np.uint8))
+
+
+def test_bf4_brute_force_nearest_and_c():
+    rng = np.random.RandomState(43)
+    for trial in range(300):
+        scale = 10.0 ** rng.uniform(-6, 4)
+        words = _bf16_words(rng, (1, 16), scale)
+        vals = [float(x) for x in bf16.bits_to_f32(words)[0]]
+        q, e8 = bfp8.quantize(words, mantissa_bits=3)
+        shared = max(math.frexp(v)[1] for v in vals if v != 0)
+        assert int(e8[0, 0]) == shared + 124
+        s = 2.0 ** (shared - 3)
+        for v, got in zip(vals, q[0]):
+            best = min(range(-7, 8), key=lambda c: (abs(v - c * s), c % 2))
+            assert int(got) == best, (trial, v, s, got, best)
+    w = _bf16_words(rng, (48, 512), 3e-3)
+    qn, en = bfp8.quantize(w, mantissa_bits=3)
+    qc, ec = c_oracle.quantize(w, mantissa_bits=3)
+    assert np.array_equal(qn, qc) and np.array_equal(en, ec)
+    assert bfp8.bf8_exact(bfp8.dequantize(qn, en), mantissa_bits=3)
+
+
+def test_bf4_tile_layout():
+    """pack_tiles_bf4 is lossless and puts a value where the layout description says."""
+    rng = np.random.RandomState(47)
+    rows, cols = 32, 512
+    q, e8 = bfp8.quantize(_bf16_words(rng, (rows, cols), 0.02), mantissa_bits=3)
+    tiles, rowexp, flushed = bfp8.pack_tiles_bf4(q, e8)
+    assert flushed == 0
+    assert tiles.size + rows * 4 + bfp8.TRAILER_BYTES == bfp8.packed_bytes(rows, cols, "bf4")
+    assert np.array_equal(bfp8.dequant_tiles_bf4(tiles, rowexp, rows, cols), bfp8.dequantize(q, e8))
+    # spot check: row 21 (tile 1, r 5), K = 256 + 64*3 + 16*2 + 13 (sb 1, step 3, quarter 2, v13)
+    r, k = 21, 256 + 64 * 3 + 16 * 2 + 13
+    lane = 2 * 16 + 5
+    blk = tiles.reshape(-1, bfp8.BF4_BLOCK_BYTES)[1 * (cols // 256) + 1]
+    byte = blk[1024 * (3 // 2) + 16 * lane + 8 * (3 % 2) + 4 + (13 - 12)]  # second dword, u_{12+1} high nibble
+    assert (byte >> 4) == q[r, k] + 8
+    with pytest.raises(ValueError):
+        bfp8.pack_tiles_bf4(np.full((16, 256), 9, np.int8), np.ones((16, 16), np.uint8))
