@@ -11,7 +11,7 @@ per-kernel HIP events on the forward's stream times the dominant (gate/up) kerne
 
 Prints one JSON line: metric, value (achieved HBM GB/s of the whole layer, algorithmic bytes
 W + 4*M*H), ms_per_step, the gate/up kernel's roofline, the CPU baseline (the oracle's torch fp32
-formula on this host's cores) and, unless --no-extras, the bf16-weight variant, the M = 1/32
+formula on this host's cores) and, unless --no-extras, the bf16-weight variant, the bf4 gate/up variant, the M = 1/32
 sweep, a 64-layer stack and the M = 2048 prefill chunk.
 """
 import argparse
@@ -221,7 +221,7 @@ def main():
     _, kern = time_layers(pkg, layers, x, args.steps, args.warmup, profile=True)
     layer_bytes = wl.algorithmic_bytes()
     value = layer_bytes / (ms / 1e3) / 1e9
-    per = 17 / 16 if wl.fmt == "bfp8" else 2
+    per = {"bfp8": 17 / 16, "bf4": 9 / 16, "bf16": 2}[wl.fmt]  # gate/up bytes per weight value
     gu_bytes = int(2 * wl.hidden * wl.intermediate * per + 2 * wl.tokens * wl.hidden)
     gu_ms = kern["gate_up"]
     gu_gbs = gu_bytes / (gu_ms / 1e3) / 1e9
@@ -239,7 +239,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16-mfma/f32-acc (bfp8 weights)" if wl.fmt == "bfp8" else "bf16-mfma/f32-acc",
+        "dtype": {"bfp8": "f16-mfma/f32-acc (bfp8 weights)", "bf4": "f16-mfma/f32-acc (bf4 gate/up, bfp8 down)",
+                  "bf16": "bf16-mfma/f32-acc"}[wl.fmt],
         "data": "synthetic: x ~ N(0,1)*U(0.5,1.5) gain, random-init weights N(0,0.02), seeds 1000/2000+",
         "config": {"workload": wl.name, "hidden": wl.hidden, "intermediate": wl.intermediate,
                    "tokens": wl.tokens, "weight_format": wl.fmt, "layers_rotated": args.rotate,
@@ -266,6 +267,22 @@ def main():
             extras["bf16_variant"] = {"us_per_layer": round(msb * 1e3, 2),
                                       "gbs": round(wb.algorithmic_bytes() / (msb / 1e3) / 1e9, 2),
                                       "bfp8_speedup": round(msb / ms, 3)}
+            # bf4 gate/up + bfp8 down (the reference's weight formats) at the same width
+            w4 = workloads.Workload(wl.name.replace("bfp8", "bf4"), wl.hidden, wl.intermediate, wl.tokens, "bf4",
+                                    wl.gain)
+            _log("bf4 gate/up variant")
+            l4 = make_layers(pkg, workloads, w4, args.rotate, dev)
+            ms4, _ = time_layers(pkg, l4, x, max(50, args.steps // 2), 10)
+            _, k4 = time_layers(pkg, l4, x, max(50, args.steps // 2), 10, profile=True)
+            del l4
+            torch.cuda.empty_cache()
+            gu4 = int(2 * w4.hidden * w4.intermediate * 9 / 16 + 2 * w4.tokens * w4.hidden)
+            extras["bf4_variant"] = {"us_per_layer": round(ms4 * 1e3, 2),
+                                     "gbs": round(w4.algorithmic_bytes() / (ms4 / 1e3) / 1e9, 2),
+                                     "algorithmic_bytes_per_layer": w4.algorithmic_bytes(),
+                                     "kernel_ms": {k: round(v, 5) for k, v in k4.items()},
+                                     "gate_up_gbs": round(gu4 / (k4["gate_up"] / 1e3) / 1e9, 2),
+                                     "speedup_vs_bfp8": round(ms / ms4, 3)}
             # width sweep
             sweep = {}
             lq = make_layers(pkg, workloads, wl, args.rotate, dev)

@@ -14,15 +14,16 @@
 //
 // Inside a workgroup:
 //   1. the token activations of its K range are staged once into LDS in the matrix-core B
-//      operand order (bfp8: converted bf16 -> fp16 with a per-(token, K range) power of two);
+//      operand order (block-float weights: converted bf16 -> fp16 with a per-(token, K range)
+//      power of two);
 //   2. the 8 waves split the rectangle's units (tile-major) into equal contiguous ranges and
 //      stream their weight blocks (ping-pong register stages, non-temporal 16-byte loads),
 //      dequantising in registers; partial sums are parked in LDS at tile boundaries;
 //   3. after one barrier each tile's partials are summed in wave order and published to a
 //      workspace slot; each thread waits for its stores, then one arrival counter per workgroup;
 //   4. the last of the S workgroups of a tile group sums the S slots in K order (deterministic)
-//      and runs the epilogue: gate/up -> h = silu(g) * u (bf16, or fp16 * 2^th for bfp8),
-//      down -> out = residual + y (bf16 or fp32).  It resets the counter for the next call.
+//      and runs the epilogue: gate/up -> h = silu(g) * u (bf16, or fp16 * 2^th for block-float
+//      weights), down -> out = residual + y (bf16 or fp32).  It resets the counter for the next call.
 #include <algorithm>
 #include <map>
 #include <mutex>
@@ -41,19 +42,19 @@ struct GvParams {
   const uint16_t* src;  // activations [M, K] row-major: x (bf16) for gate/up, h for down
   int M, K, N;
   int C, T, G, S, KQ, Ng, P, maxseg;
-  int x_scale;            // 1: src is bf16 and is converted to fp16 * 2^t (bfp8 gate/up)
+  int x_scale;            // 1: src is bf16 and is converted to fp16 * 2^t (block-float gate/up)
   const uint16_t* normw;  // gate/up with the RMSNorm prologue: bf16 [K] weight w (gain 1 + w)
   float eps;              //   and its epsilon
-  const int* th_in;       // bfp8 down: h = h16 * 2^-th[m]
-  int* th_out;            // bfp8 gate/up: th[m] written by tile group 0
-  const Trailer* tg;      // bfp8 gate/up: weight row-norm trailers for the h bound
+  const int* th_in;       // block-float down: h = h16 * 2^-th[m]
+  int* th_out;            // block-float gate/up: th[m] written by tile group 0
+  const Trailer* tg;      // block-float gate/up: weight row-norm trailers for the h bound
   const Trailer* tu;
   void* out;              // gate/up: h [M, N] 16-bit; down: out [M, N] bf16 or fp32
   const void* residual;   // down: [M, N] bf16 or fp32, may alias out
   int out_f32, res_f32;
   float* part;            // [P][G][NMAT * 64] f32x4 partial slots
   float* pss;             // [P][32] per-workgroup token sums: [0,16) of the staged values'
-                          // squares (bfp8 h bound), [16,32) of the raw x squares (RMSNorm)
+                          // squares (h bound), [16,32) of the raw x squares (RMSNorm)
   int* counters;          // [Ng] arrival counters (left at zero)
 };
 

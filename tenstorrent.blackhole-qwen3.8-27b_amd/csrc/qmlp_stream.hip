@@ -6,9 +6,10 @@
 // by the widened down projection (scripts/ci/mlp_down_grid.py:4-12) and the layer's residual add
 // (docker/qwen-c2-graft/graft/layer.py:357).
 //
-// Operands.  Both weight formats feed bf16 matrix-core products with fp32 accumulation: bf16
-// weights as they are, bfp8 weights dequantised in registers (a byte u and its group scale s give
-// (u - 128) * s, at most 8 significant bits, so the bf16 value is exact).  The tokens are the
+// Operands.  Every weight format feeds bf16 matrix-core products with fp32 accumulation: bf16
+// weights as they are, bfp8 and bf4 weights dequantised in registers (a mantissa u and its group
+// scale s give (u - 128) * s, resp. (u - 8) * s, at most 8 significant bits, so the bf16 value is
+// exact).  The tokens are the
 // B operand, read by each wave straight from L2 in the matrix-core lane order (token rows are
 // small and shared by every workgroup), so no workgroup stages activations and h stays bf16 --
 // the reference's own rounding of h.
