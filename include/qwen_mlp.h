@@ -124,7 +124,8 @@ int qmlp_dequant_packed(const void* packed, int rows, int cols, int fmt, float* 
  *   ws       workspace of at least qmlp_workspace_bytes(M, H, I, fmt) bytes, initialised once by
  *            qmlp_workspace_init; the kernels leave it re-usable.  Concurrent forwards need
  *            separate workspaces.
- * Constraints: H and I multiples of 256; 1 <= M <= 65536; pointers 16-byte aligned.
+ * Constraints: H and I multiples of 256; 1 <= M <= 65536 and M * max(H, I) < 2^30; pointers
+ * 16-byte aligned.
  * M <= 32 uses the weight-streaming kernels; larger M the LDS-tiled matrix-core kernels. */
 int qmlp_forward(const void* x, const void* wg, const void* wu, const void* wd,
                  const void* residual, void* out, void* ws, size_t ws_bytes, int M, int H, int I,

@@ -236,6 +236,10 @@ static int forward_impl(const char* fn, const void* x, const void* wg, const voi
   if (M < 1 || M > 65536) return set_error(QMLP_E_SHAPE, "%s: M=%d out of range [1, 65536]", fn, M);
   if (!shape_ok(16, H) || !shape_ok(16, I))
     return set_error(QMLP_E_SHAPE, "%s: H=%d and I=%d must be positive multiples of 256", fn, H, I);
+  // the kernels address one activation matrix ([M, H] or [M, I], up to fp32) with 32-bit offsets
+  if ((uint64_t)M * (uint64_t)std::max(H, I) * 4u >= (1ull << 32))
+    return set_error(QMLP_E_SHAPE, "%s: M * max(H, I) = %llu exceeds 2^30 elements", fn,
+                     (unsigned long long)M * (unsigned long long)std::max(H, I));
   if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(ws) ||
       (residual && !aligned16(residual)) || (normw && !aligned16(normw)))
     return set_error(QMLP_E_ALIGN, "%s: every pointer must be 16-byte aligned", fn);

@@ -27,7 +27,9 @@
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <set>
 #include <tuple>
+#include <utility>
 
 #include "qmlp_common.h"
 #include "qmlp_internal.h"
@@ -575,15 +577,24 @@ int plan_gemv(int rows, int K, int nmat, int num_cus, GemvPlan* out) {
   return 0;
 }
 
+// Raises a kernel's dynamic LDS limit to kGemvMaxLds, once per (kernel, device); thread-safe.
+static int enable_large_lds(const void* kern, const char* what) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(-7, "%s: no HIP device", what);
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({kern, dev})) return 0;
+  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLds) != hipSuccess)
+    return set_error(-4, "%s: cannot enable %d bytes of LDS", what, kGemvMaxLds);
+  done.insert({kern, dev});
+  return 0;
+}
+
 template <int WF, int NMAT, int MAXCH, bool NORM>
 static int launch_gemv_ch(const GvParams& p, size_t lds, hipStream_t s) {
   auto kern = gemv_kernel<WF, NMAT, kGemvNW, MAXCH, NORM>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxLds) != hipSuccess)
-      return set_error(-4, "gemv_kernel: cannot enable 160 KB LDS");
-    attr_set = true;
-  }
+  if (int rc = enable_large_lds((const void*)kern, "gemv_kernel")) return rc;
   hipLaunchKernelGGL(kern, dim3(p.P), dim3(kGemvNW * 64), lds, s, p);
   return check_launch("gemv_kernel");
 }

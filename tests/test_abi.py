@@ -76,6 +76,9 @@ def test_forward_argument_errors_need_no_gpu(pkg):
     assert lib.qmlp_forward(p, p, p, p, None, p, p, ws, 4, 256, 512, 1, None) == -1   # out aliases x
     assert lib.qmlp_forward(p, p, p, p, None, big, p, ws - 256, 4, 256, 512, 1, None) == -5
     assert b"workspace" in lib.qmlp_last_error()
+    # activations addressed with 32-bit offsets: M * max(H, I) must stay below 2^30
+    assert lib.qmlp_forward(p, p, p, p, None, big, p, 1 << 62, 65536, 256, 16384, 1, None) == -1
+    assert b"2^30" in lib.qmlp_last_error()
     assert lib.qmlp_pack(p, None, 16, 256, 1, p, 1 << 20, None) == -6
     assert lib.qmlp_pack(p, p, 17, 256, 1, p, 1 << 20, None) == -1
     assert lib.qmlp_pack(p, p, 16, 256, 1, p, 10, None) == -5
