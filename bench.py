@@ -60,9 +60,9 @@ def time_layers(pkg, layers, x, steps, warmup, profile=False, chain=True):
     """Runs `steps` forwards cycling through `layers`; returns (ms_per_step, kernel_ms dict).
 
     chain: each layer's residual is the previous layer's output (a residual stream, as in the
-    decoder); x, the normalised MLP input, stays the same tensor.  profile: per-kernel HIP events
-    on the forward's stream (they add a little time of their own, so the headline pass runs
-    without them)."""
+    decoder); x, the normalised MLP input, stays the same tensor.  profile: each projection kernel
+    is launched with a start / stop HIP event pair (hipExtLaunchKernel: the dispatch's own
+    timestamps on the forward's stream); the headline pass runs without them."""
     import ctypes
 
     import torch
@@ -99,9 +99,8 @@ def time_layers(pkg, layers, x, steps, warmup, profile=False, chain=True):
     ms = start.elapsed_time(end) / steps
     kern = {}
     if profile:
-        names = ("prep", "gate_up", "down")
-        for k, name in enumerate(names):
-            kern[name] = statistics.fmean(ev[k].elapsed_time(ev[k + 1]) for ev in events)
+        for k, name in enumerate(("gate_up", "down")):
+            kern[name] = statistics.fmean(ev[2 * k].elapsed_time(ev[2 * k + 1]) for ev in events)
     return ms, kern
 
 

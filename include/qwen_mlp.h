@@ -168,10 +168,11 @@ int qmlp_workspace_init(void* ws, size_t ws_bytes, qmlp_stream_t stream);
  *
  * Per-kernel timing of the forward pass, the counterpart of the reference's per-op signposts
  * (docker/qwen-c2-graft/graft/layer.py:18-90).  When n == 4, every later qmlp_forward on this host
- * thread records events[0] before its first kernel, events[1] after the activation prep (bfp8;
- * == events[0] for bf16), events[2] after the gate/up kernel and events[3] after the down kernel,
- * on the forward's stream (hipEvent_t handles).  n == 0 turns recording off.  Only the
- * weight-streaming path (M <= 32) records. */
+ * thread launches its gate/up kernel with events[0] / events[1] as the start / stop events of
+ * hipExtLaunchKernel and its down kernel with events[2] / events[3] (hipEvent_t handles): each
+ * pair then holds the timestamps of that dispatch itself, and no marker packets are inserted
+ * between the kernels.  n == 0 turns timing off.  Kernels outside the two projections (the
+ * RMSNorm pass, the prefill's activation prep) are not timed. */
 int qmlp_set_profile_events(void* const* events, int n);
 
 /* ---------------------------------------------------------------- planning (host only)

@@ -38,8 +38,11 @@ void set_profile_events(const hipEvent_t* ev) {
     for (int i = 0; i < 4; ++i) g_prof[i] = ev[i];
 }
 
-void profile_mark(int i, hipStream_t s) {
-  if (g_prof_on) (void)hipEventRecord(g_prof[i], s);
+bool profile_events(int slot, hipEvent_t* start, hipEvent_t* stop) {
+  if (!g_prof_on || slot < 0 || slot > 1) return false;
+  *start = g_prof[2 * slot];
+  *stop = g_prof[2 * slot + 1];
+  return true;
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }

@@ -595,7 +595,7 @@ template <int WF, int NMAT, int MAXCH, bool NORM>
 static int launch_gemv_ch(const GvParams& p, size_t lds, hipStream_t s) {
   auto kern = gemv_kernel<WF, NMAT, kGemvNW, MAXCH, NORM>;
   if (int rc = enable_large_lds((const void*)kern, "gemv_kernel")) return rc;
-  hipLaunchKernelGGL(kern, dim3(p.P), dim3(kGemvNW * 64), lds, s, p);
+  launch_timed(NMAT == 2 ? 0 : 1, kern, dim3(p.P), dim3(kGemvNW * 64), lds, s, p);
   return check_launch("gemv_kernel");
 }
 
@@ -637,8 +637,6 @@ int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s) {
     return set_error(-1, "no weight-streaming split for H=%d I=%d", a.H, a.I);
   int* th = (int*)(a.ws + L.th);
   uint16_t* h = (uint16_t*)(a.ws + L.h);
-  profile_mark(0, s);
-  profile_mark(1, s);
   GvParams g{};
   g.w0 = a.wg;
   g.w1 = a.wu;
@@ -675,7 +673,6 @@ int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s) {
   else
     rc = a.normw ? launch_gemv<0, 2, true>(g, lg, s) : launch_gemv<0, 2>(g, lg, s);
   if (rc) return rc;
-  profile_mark(2, s);
   GvParams d{};
   d.w0 = a.wd;
   const int dfmt = down_format(fmt);
@@ -702,7 +699,6 @@ int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.counters = (int*)(a.ws + L.counters_d);
   rc = dfmt == 1 ? launch_gemv<1, 1>(d, gemv_lds_bytes(pd, 1), s) : launch_gemv<0, 1>(d, gemv_lds_bytes(pd, 1), s);
   if (rc) return rc;
-  profile_mark(3, s);
   return 0;
 }
 

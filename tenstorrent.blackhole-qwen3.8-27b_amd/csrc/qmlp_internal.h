@@ -1,5 +1,6 @@
 // qmlp_internal.h -- host-side declarations shared by the library's translation units.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -10,9 +11,23 @@ namespace qmlp {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
-// Optional per-kernel events of the forward pass (qmlp_set_profile_events).
+// Optional per-kernel timing of the forward pass (qmlp_set_profile_events): slot 0 is the
+// gate/up kernel, slot 1 the down kernel.  profile_events() hands out the slot's start / stop
+// events while timing is on.
 void set_profile_events(const hipEvent_t* ev);
-void profile_mark(int i, hipStream_t s);
+bool profile_events(int slot, hipEvent_t* start, hipEvent_t* stop);
+
+// Launches a hot-path kernel.  While timing is on, the launch goes through hipExtLaunchKernel so
+// that the dispatch's own start and end timestamps land in the slot's events (no marker packets
+// between the kernels, so the timed kernels run exactly as they do untimed).
+template <typename... Args>
+void launch_timed(int slot, void (*kern)(Args...), dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+  hipEvent_t start, stop;
+  if (profile_events(slot, &start, &stop))
+    hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)lds, s, start, stop, 0u, args...);
+  else
+    hipLaunchKernelGGL(kern, grid, block, lds, s, args...);
+}
 
 // Load-time kernels (qmlp_pack.hip).
 int launch_quantize(const void* w, int rows, int cols, void* q, void* e8, uint32_t* bad, int mbits, hipStream_t s);

@@ -349,7 +349,7 @@ bool stream_supported(int M, int H, int I, int num_cus) {
 template <int WF, int NMAT, int MG>
 static int launch_stream(const StParams& p, hipStream_t s) {
   const size_t lds = (size_t)kStNW * p.maxseg * NMAT * MG * 64 * 16;
-  hipLaunchKernelGGL((stream_kernel<WF, NMAT, MG, kStNW>), dim3(p.P), dim3(kStNW * 64), lds, s, p);
+  launch_timed(NMAT == 2 ? 0 : 1, stream_kernel<WF, NMAT, MG, kStNW>, dim3(p.P), dim3(kStNW * 64), lds, s, p);
   return check_launch("stream_kernel");
 }
 
@@ -365,8 +365,6 @@ int launch_forward_stream(const ForwardArgs& a, int num_cus, hipStream_t s) {
   if (plan_stream(a.I, a.H, num_cus, &Pg, &mg) || plan_stream(a.H, a.I, num_cus, &Pd, &md))
     return set_error(-1, "no weight-streaming split for H=%d I=%d", a.H, a.I);
   uint16_t* h = (uint16_t*)(a.ws + L.h);
-  profile_mark(0, s);
-  profile_mark(1, s);
   StParams g{};
   g.w0 = a.wg;
   g.w1 = a.wu;
@@ -386,7 +384,6 @@ int launch_forward_stream(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.counters = (int*)(a.ws + L.counters_gu);
   int rc = fmt == 2 ? launch_stream_m<2, 2>(g, s) : (fmt == 1 ? launch_stream_m<1, 2>(g, s) : launch_stream_m<0, 2>(g, s));
   if (rc) return rc;
-  profile_mark(2, s);
   StParams d{};
   d.w0 = a.wd;
   const int dfmt = down_format(fmt);
@@ -408,7 +405,6 @@ int launch_forward_stream(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.counters = (int*)(a.ws + L.counters_d);
   rc = dfmt == 1 ? launch_stream_m<1, 1>(d, s) : launch_stream_m<0, 1>(d, s);
   if (rc) return rc;
-  profile_mark(3, s);
   return 0;
 }
 

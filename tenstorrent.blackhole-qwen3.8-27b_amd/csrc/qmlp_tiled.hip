@@ -267,7 +267,8 @@ template <int WF, int NMAT, int TPW>
 static int launch_tiled(const TlParams& p, hipStream_t s) {
   const int nbn = p.N / (kTlNWV * TPW * kTileRows);
   const size_t lds = (size_t)3 * kTlMG * 2048;
-  hipLaunchKernelGGL((tiled_kernel<WF, NMAT, TPW, kTlMG, kTlNWV>), dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s, p);
+  launch_timed(NMAT == 2 ? 0 : 1, tiled_kernel<WF, NMAT, TPW, kTlMG, kTlNWV>, dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds,
+               s, p);
   return check_launch("tiled_kernel");
 }
 
@@ -288,12 +289,10 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   int* th = (int*)(a.ws + L.th);
   uint16_t* x16 = (uint16_t*)(a.ws + L.x16);
   uint16_t* h = (uint16_t*)(a.ws + L.h);
-  profile_mark(0, s);
   if (fmt != 0) {
     int rc = launch_prep(a, s);
     if (rc) return rc;
   }
-  profile_mark(1, s);
   const int nbm = (a.M + kTlMG * 16 - 1) / (kTlMG * 16);
   TlParams g{};
   g.w0 = a.wg;
@@ -311,7 +310,6 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.out = h;
   int rc = fmt == 2 ? launch_tiled<2, 2, 2>(g, s) : (fmt == 1 ? launch_tiled<1, 2, 2>(g, s) : launch_tiled<0, 2, 2>(g, s));
   if (rc) return rc;
-  profile_mark(2, s);
   TlParams d{};
   d.w0 = a.wd;
   const int dfmt = down_format(fmt);
@@ -329,7 +327,6 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.res_f32 = a.res_f32;
   rc = dfmt == 1 ? launch_tiled<1, 1, 2>(d, s) : launch_tiled<0, 1, 2>(d, s);
   if (rc) return rc;
-  profile_mark(3, s);
   return 0;
 }
 
