@@ -184,11 +184,12 @@ int qmlp_set_profile_events(void* const* events, int n);
  * (scripts/ci/test_fused_1d.py:71-79). */
 int qmlp_plan_stream(int rows, int K, int num_cus, int* out2);
 
-/* Work split of the M <= 16 kernel for one projection with `nmat` matrices (2 = gate/up,
- * 1 = down): the (16-row tile x 256-K superblock) grid cut into tile groups x K splits.
- * Fills out[0..5] = {workgroups, tiles per group, K splits, superblocks per split, groups,
- * tiles one wave may touch}. */
-int qmlp_plan_split(int rows, int K, int nmat, int num_cus, int* out6);
+/* Work split of the M <= 32 weight-streaming kernel for one projection with `nmat` matrices
+ * (2 = gate/up, 1 = down) at M tokens (1..32; 17..32 run as two groups of 16): the (16-row tile
+ * x 256-K superblock) grid cut into tile groups x K splits, split q covering superblocks
+ * [q*C/S, (q+1)*C/S) of C = K/256.  Fills out[0..5] = {workgroups, tiles per group, K splits,
+ * superblocks of the longest split, groups, tiles one wave may touch}. */
+int qmlp_plan_split(int rows, int K, int nmat, int M, int num_cus, int* out6);
 
 #ifdef __cplusplus
 }

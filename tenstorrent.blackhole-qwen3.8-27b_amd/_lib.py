@@ -39,7 +39,7 @@ SIGNATURES = {
     "qmlp_workspace_init": (_I, [_P, _SZ, _P]),
     "qmlp_plan_stream": (_I, [_I, _I, _I, ctypes.POINTER(ctypes.c_int)]),
     "qmlp_set_profile_events": (_I, [_P, _I]),
-    "qmlp_plan_split": (_I, [_I, _I, _I, _I, ctypes.POINTER(ctypes.c_int)]),
+    "qmlp_plan_split": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int)]),
     "qmlp_forward_rmsnorm": (_I, [_P, _P, ctypes.c_float, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _P]),
 }
 

@@ -63,17 +63,17 @@ WsLayout ws_layout(int M, int H, int I, int fmt) {
   L.h = off;
   off = align256(off + (size_t)M * I * 2);
   // partial-sum slots: the stream-K kernel (M <= 32) needs 2 per workgroup of NMAT x 2 token
-  // groups x 64 lanes x 16 B, the split kernel (M <= 16) one per (workgroup, tile) of NMAT x 1 KB
+  // groups x 64 lanes x 16 B, the split kernel (M <= 32) one per (workgroup, tile) of NMAT x MG KB
   const size_t sk_gu = (size_t)2 * kMaxWorkgroups * (2 * 2 * 64 * 16);
   const size_t sk_d = (size_t)2 * kMaxWorkgroups * (1 * 2 * 64 * 16);
-  const size_t gv_gu = gemv_max_slots(I, H, 2) * (2 * 64 * 16);
-  const size_t gv_d = gemv_max_slots(H, I, 1) * (1 * 64 * 16);
+  const size_t gv_gu = M <= 32 ? gemv_part_bytes(I, H, 2, gemv_groups(M)) : 0;
+  const size_t gv_d = M <= 32 ? gemv_part_bytes(H, I, 1, gemv_groups(M)) : 0;
   L.part_gu = off;
   off = align256(off + std::max(sk_gu, gv_gu));
   L.part_d = off;
   off = align256(off + std::max(sk_d, gv_d));
   L.pss = off;
-  off = align256(off + (size_t)kMaxWorkgroups * 32 * 4);
+  off = align256(off + (size_t)kMaxWorkgroups * 64 * 4);
   L.xn = off;  // bf16 [M, H]: the normalised activations when the RMSNorm runs as its own pass
   off = align256(off + (size_t)M * H * 2);
   L.total = off;
@@ -266,9 +266,10 @@ static int forward_impl(const char* fn, const void* x, const void* wg, const voi
   if (int rc = current_device_info(&di)) return rc;
   ForwardArgs a{x, (const uint8_t*)wg, (const uint8_t*)wu, (const uint8_t*)wd, residual, out, (uint8_t*)ws,
                 M, H, I, fmt, (flags & QMLP_OUT_F32) ? 1 : 0, (flags & QMLP_RESIDUAL_F32) ? 1 : 0, normw, eps};
-  // M <= 16: split-K weight streaming with LDS-staged activations (the RMSNorm fused into its
-  // staging and epilogue); M <= 32: stream-K weight streaming with activations read from L2;
-  // larger M: the LDS-tiled matrix-core GEMM.  The last two take the RMSNorm as a separate pass.
+  // M <= 32: split-K weight streaming with LDS-staged activations (the RMSNorm fused into its
+  // staging and epilogue); where no such split fits (very small devices), M <= 32: stream-K
+  // weight streaming with activations read from L2; larger M: the LDS-tiled matrix-core GEMM.
+  // The last two take the RMSNorm as a separate pass.
   if (gemv_supported(M, H, I, di.num_cus)) return launch_forward_gemv(a, di.num_cus, (hipStream_t)stream);
   if (normw) {
     uint8_t* xn = (uint8_t*)ws + L.xn;
@@ -311,10 +312,12 @@ int qmlp_set_profile_events(void* const* events, int n) {
   return 0;
 }
 
-int qmlp_plan_split(int rows, int K, int nmat, int num_cus, int* out6) {
+int qmlp_plan_split(int rows, int K, int nmat, int M, int num_cus, int* out6) {
   if (!out6) return set_error(QMLP_E_NULL, "qmlp_plan_split: null pointer");
+  if (M < 1 || M > 32) return set_error(QMLP_E_SHAPE, "qmlp_plan_split: M=%d out of range [1, 32]", M);
   GemvPlan p;
-  if (plan_gemv(rows, K, nmat, num_cus, &p)) return set_error(QMLP_E_SHAPE, "qmlp_plan_split: no split for %dx%d", rows, K);
+  if (plan_gemv(rows, K, nmat, gemv_groups(M), num_cus, &p))
+    return set_error(QMLP_E_SHAPE, "qmlp_plan_split: no split for %dx%d at M=%d", rows, K, M);
   out6[0] = p.P;
   out6[1] = p.G;
   out6[2] = p.S;

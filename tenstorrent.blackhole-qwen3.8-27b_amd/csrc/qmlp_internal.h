@@ -38,20 +38,22 @@ int launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 
 constexpr int kMaxWorkgroups = 512;  // upper bound used to size the workspace
 
-// 2-D split of one projection for the M <= 16 weight-streaming kernel (qmlp_gemv.hip).
+// 2-D split of one projection for the M <= 32 weight-streaming kernel (qmlp_gemv.hip).
 struct GemvPlan {
   int G;       // tiles per group
   int S;       // K splits
-  int KQ;      // superblocks per K split
+  int KQ;      // superblocks of the longest K split (splits differ by at most one)
   int Ng;      // tile groups
   int P;       // workgroups = Ng * S
   int maxseg;  // tiles one wave may touch
 };
 constexpr int kMaxSplit = 16;
-int plan_gemv(int rows, int K, int nmat, int num_cus, GemvPlan* out);
+// mg: groups of 16 tokens (1 for M <= 16, 2 for M <= 32).
+int plan_gemv(int rows, int K, int nmat, int mg, int num_cus, GemvPlan* out);
+int gemv_groups(int M);
 bool gemv_supported(int M, int H, int I, int num_cus);
-// Largest partial-slot count (P * G) any device could need for this projection (workspace size).
-size_t gemv_max_slots(int rows, int K, int nmat);
+// Largest partial-slot buffer any device could need for this projection (workspace size).
+size_t gemv_part_bytes(int rows, int K, int nmat, int mg);
 
 // Workspace layout for one forward call.
 struct WsLayout {

@@ -139,32 +139,55 @@ def test_stream_split_covers_every_step_once(pkg, rows, K):
 
 @pytest.mark.parametrize("rows,K", SHAPES)
 @pytest.mark.parametrize("nmat", [1, 2])
-def test_gemv_split_covers_every_unit_once(pkg, rows, K, nmat):
-    """M <= 16 kernel: tile groups x K splits cover every (tile, superblock) unit once, each
-    workgroup's waves split its rectangle exactly, and no wave touches more than maxseg tiles."""
+@pytest.mark.parametrize("M", [16, 32])
+def test_gemv_split_covers_every_unit_once(pkg, rows, K, nmat, M):
+    """M <= 32 kernel: tile groups x K splits (split q = superblocks [q*C/S, (q+1)*C/S)) cover every
+    (tile, superblock) unit once, each workgroup's waves split its rectangle exactly, no wave
+    touches more than maxseg tiles, and the staged activations fit the register chunks."""
+    mg = 1 if M <= 16 else 2
     for cus in CUS:
         out = (ctypes.c_int * 6)()
-        rc = pkg.lib().qmlp_plan_split(rows, K, nmat, cus, out)
+        rc = pkg.lib().qmlp_plan_split(rows, K, nmat, M, cus, out)
         if rc != 0:
             continue  # no split fits (K too long for the staged activations): the caller falls back
         P, G, S, KQ, Ng, maxseg = list(out)
         T, C = rows // 16, K // 256
-        assert S * KQ == C and Ng == -(-T // G) and P == Ng * S and P <= max(cus, 1)
+        assert KQ == -(-C // S) and KQ * mg <= 18 and maxseg <= 12 // (nmat * mg)
+        assert Ng == -(-T // G) and P == Ng * S and P <= max(cus, 1)
         covered = [[0] * C for _ in range(T)]
         for w in range(P):
             g, q = w // S, w % S
+            c0, c1 = q * C // S, (q + 1) * C // S
+            kq = c1 - c0
+            assert kq in (KQ, KQ - 1) and kq >= 1
             Gw = min(G, T - g * G)
-            U = Gw * KQ
+            U = Gw * kq
             done = 0
             for v in range(8):
                 ua, ub = v * U // 8, (v + 1) * U // 8
                 if ua < ub:
-                    assert (ub - 1) // KQ - ua // KQ + 1 <= maxseg
+                    assert (ub - 1) // kq - ua // kq + 1 <= maxseg
                 for u in range(ua, ub):
-                    covered[g * G + u // KQ][q * KQ + u % KQ] += 1
+                    covered[g * G + u // kq][c0 + u % kq] += 1
                 done += ub - ua
             assert done == U
         assert all(c == 1 for row in covered for c in row)
+
+
+def test_plan_split_rejects_bad_widths(pkg):
+    out = (ctypes.c_int * 6)()
+    assert pkg.lib().qmlp_plan_split(17408, 5120, 2, 0, 256, out) != 0
+    assert pkg.lib().qmlp_plan_split(17408, 5120, 2, 33, 256, out) != 0
+
+
+def test_gemv_split_at_the_27b_shape(pkg):
+    """The splits quoted for the Qwen3-27B shape on 256 CUs."""
+    out = (ctypes.c_int * 6)()
+    want = {(17408, 5120, 2, 16): (242, 9, 2, 10), (5120, 17408, 1, 16): (256, 5, 4, 17),
+            (17408, 5120, 2, 32): (252, 13, 3, 7), (5120, 17408, 1, 32): (256, 10, 8, 9)}
+    for (rows, K, nmat, M), (P, G, S, KQ) in want.items():
+        assert pkg.lib().qmlp_plan_split(rows, K, nmat, M, 256, out) == 0
+        assert tuple(out)[:4] == (P, G, S, KQ), (rows, K, nmat, M, tuple(out))
 
 
 def test_pack_checkpoint_finds_mlp_weights(tmp_path, pkg):

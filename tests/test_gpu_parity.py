@@ -222,6 +222,29 @@ def test_forward_every_small_width(pkg, cuda, fmt):
         _check(y.cpu().numpy(), _oracle(xf, hw), f"{fmt} H={H} I={I} M={M}")
 
 
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
+def test_forward_stream_fallback(pkg, cuda, fmt):
+    """A down projection too long for the split kernel's staged activations (K = 76800 > 16 splits
+    x 18 superblocks) takes the stream-K weight-streaming kernels instead, at every width."""
+    import ctypes
+
+    import torch
+    from qwen_mlp_amd import workloads
+
+    H, I = 256, 76800
+    out = (ctypes.c_int * 6)()
+    assert pkg.lib().qmlp_plan_split(H, I, 1, 16, 256, out) != 0
+    sd = workloads.state_dict(H, I, layer=4, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=32)
+    hw = _host_weights(pkg, sd, fmt)
+    for M in (1, 16, 17, 32):
+        print(f"case stream fallback {fmt} M={M}", flush=True)
+        x = workloads.activations(M, H, seed=4100 + M, device=cuda)
+        y = mlp.forward(x, residual=x, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        _check(y.cpu().numpy(), _oracle(x.float().cpu().numpy(), hw), f"stream fallback {fmt} M={M}")
+
+
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 def test_zero_input_and_aliasing(pkg, cuda, fmt):
     import torch
@@ -346,7 +369,7 @@ def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
 def test_rmsnorm_prologue(pkg, cuda, fmt):
     """h + MLP(rmsnorm(h) * (1 + w)) against the oracle's composition (the norm output rounded to
     bf16 as the reference's separate norm produces it), across every dispatch width: fused into
-    the M <= 16 kernel, a separate pass for the others; then in place (out = h)."""
+    the M <= 32 weight-streaming kernel, a separate pass for the others; then in place (out = h)."""
     import torch
     from qwen_mlp_amd import workloads
 
