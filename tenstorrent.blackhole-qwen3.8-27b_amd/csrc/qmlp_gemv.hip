@@ -13,9 +13,8 @@
 // products.  At the Qwen3-27B shape:
 //   16 tokens: gate/up 121 groups of 9 tiles x 2 halves of 10 superblocks (242 workgroups of 90
 //              units), down 64 groups of 5 tiles x 4 quarters of 17 (256 workgroups of 85 units);
-//   32 tokens: gate/up 84 groups of 13 tiles x 3 thirds of 6 or 7 superblocks (252 workgroups of
-//              at most 91 units), down 32 groups of 10 tiles x 8 eighths of 8 or 9 (256 x at
-//              most 90 units).
+//   32 tokens: gate/up 64 groups of 17 tiles x 4 quarters of 5 superblocks (256 workgroups of 85
+//              units), down 32 groups of 10 tiles x 8 eighths of 8 or 9 (256 x at most 90 units).
 //
 // Inside a workgroup:
 //   1. the token activations of its K range are staged once into LDS in the matrix-core B
@@ -746,9 +745,11 @@ static size_t gemv_lds_bytes(const GemvPlan& pl, int nmat, int mg) {
 
 // Work split: minimise a simple time model over the K split S.  A workgroup streams U = G * KQ
 // units (NMAT x 4352-byte blocks each); the last workgroup of a tile group then reads S * G
-// partial tiles (NMAT x MG KB each).  Units cost ~0.16 us per matrix at a CU's share of HBM
-// bandwidth, partial tiles ~0.05 us per KB (measured on MI355X); splits using fewer than all
-// CUs pay for it through their larger U.  K splits may differ by one superblock.
+// partial tiles per matrix.  Units cost ~0.16 us per matrix at a CU's share of HBM bandwidth,
+// partial tiles ~0.03 us each whatever the token groups (fitted on MI355X to the measured
+// 27B-shape splits: at 16 tokens gate/up 2 K splits beat 4, at 32 tokens 4 beat 3, and down 8
+// beat 10); splits using fewer than all CUs pay for it through their larger U.  K splits may
+// differ by one superblock.
 int plan_gemv(int rows, int K, int nmat, int mg, int num_cus, GemvPlan* out) {
   if (rows <= 0 || K <= 0 || rows % kTileRows || K % kSuperK || (mg != 1 && mg != 2) || (nmat != 1 && nmat != 2))
     return -1;
@@ -779,7 +780,7 @@ int plan_gemv(int rows, int K, int nmat, int mg, int num_cus, GemvPlan* out) {
     GemvPlan c{G, S, KQ, Ng, P, maxseg};
     if (gemv_lds_bytes(c, nmat, mg) > (size_t)kGemvMaxLds) continue;
     const int U = G * KQ;
-    const double cost = U * 0.16 * nmat + (S > 1 ? S * G * nmat * mg * 0.05 : 0.0);
+    const double cost = U * 0.16 * nmat + (S > 1 ? S * G * nmat * 0.03 : 0.0);
     if (best_cost < 0 || cost < best_cost - 1e-9) {
       best = c;
       best_cost = cost;
