@@ -151,9 +151,10 @@ int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* w
  *   h       bf16 [M, H], the pre-norm hidden state (also the residual)
  *   norm_w  bf16 [H]
  *   out     bf16 [M, H] (fp32 with QMLP_OUT_F32); may equal h (in-place residual update)
- * Other arguments and constraints as qmlp_forward_ex (QMLP_RESIDUAL_F32 is not accepted).  M <= 16
+ * Other arguments and constraints as qmlp_forward_ex (QMLP_RESIDUAL_F32 is not accepted).  M <= 32
  * fuses the norm into the gate/up kernel (the channel gain into the activation staging, the
- * per-token 1/rms into the epilogue); larger M run it as one extra pass over h. */
+ * per-token 1/rms into the epilogue); larger M (and the long-K fallback) run it as one extra pass
+ * over h. */
 int qmlp_forward_rmsnorm(const void* h, const void* norm_w, float eps, const void* wg, const void* wu,
                          const void* wd, void* out, void* ws, size_t ws_bytes, int M, int H, int I,
                          int fmt, int flags, qmlp_stream_t stream);
@@ -177,8 +178,9 @@ int qmlp_set_profile_events(void* const* events, int n);
 
 /* ---------------------------------------------------------------- planning (host only)
  *
- * Work split of the 16 < M <= 32 (stream-K) kernel for one projection: `rows` output rows
- * (multiple of 16) over K (multiple of 256) on `num_cus` compute units.  Fills out[0..1] =
+ * Work split of the M <= 32 stream-K kernel (the fallback where qmlp_plan_split finds no split)
+ * for one projection: `rows` output rows (multiple of 16) over K (multiple of 256) on `num_cus`
+ * compute units.  Fills out[0..1] =
  * {workgroups, tiles one wave may touch}.  Exposed so the coverage of the split can be tested
  * without a GPU, like the reference's worker-to-pair mapping tests
  * (scripts/ci/test_fused_1d.py:71-79). */
