@@ -267,7 +267,8 @@ static int forward_impl(const char* fn, const void* x, const void* wg, const voi
   ForwardArgs a{x, (const uint8_t*)wg, (const uint8_t*)wu, (const uint8_t*)wd, residual, out, (uint8_t*)ws,
                 M, H, I, fmt, (flags & QMLP_OUT_F32) ? 1 : 0, (flags & QMLP_RESIDUAL_F32) ? 1 : 0, normw, eps};
   // M <= 32: split-K weight streaming with LDS-staged activations (the RMSNorm fused into its
-  // staging and epilogue); where no such split fits (very small devices), M <= 32: stream-K
+  // staging and epilogue); where no such split fits (a K too long for the staged activations, or
+  // a device too small for the split's registers), M <= 32: stream-K
   // weight streaming with activations read from L2; larger M: the LDS-tiled matrix-core GEMM.
   // The last two take the RMSNorm as a separate pass.
   if (gemv_supported(M, H, I, di.num_cus)) return launch_forward_gemv(a, di.num_cus, (hipStream_t)stream);

@@ -105,7 +105,7 @@ def _wg_of_step(s, S, P):
 
 @pytest.mark.parametrize("rows,K", SHAPES)
 def test_stream_split_covers_every_step_once(pkg, rows, K):
-    """16 < M <= 32 kernel: the workgroup and wave step ranges tile [0, S) exactly, no wave touches
+    """Stream-K fallback kernel: the workgroup and wave step ranges tile [0, S) exactly, no wave touches
     more tiles than the plan's LDS slots, the owner formula matches the ranges, and every tile
     shared by workgroups is the first or last tile of each (its partial slot) -- the reference's
     worker-to-pair coverage test (scripts/ci/test_fused_1d.py:71-79) for this split."""
