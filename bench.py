@@ -12,7 +12,7 @@ per-kernel HIP events on the forward's stream times the dominant (gate/up) kerne
 Prints one JSON line: metric, value (achieved HBM GB/s of the whole layer, algorithmic bytes
 W + 4*M*H), ms_per_step, the gate/up kernel's roofline, the CPU baseline (the oracle's torch fp32
 formula on this host's cores) and, unless --no-extras, the bf16-weight variant, the bf4 gate/up variant, the M = 1/32
-sweep, a 64-layer stack and the M = 2048 prefill chunk.
+sweep, one GPU's share of a two-way split layer, a 64-layer stack and the M = 2048 prefill chunk.
 """
 import argparse
 import json
@@ -294,6 +294,17 @@ def main():
             extras["width_sweep"] = sweep
             del lq
             torch.cuda.empty_cache()
+            # one GPU's share of a two-way (TP2) split of the layer: I = 8704 (the all-reduce of the
+            # [M, H] partials that completes the layer is not part of a one-GPU run)
+            ws2 = workloads.WORKLOADS["qwen3-27b-tp2-share-m16-bfp8"]
+            _log("TP2 share")
+            l2 = make_layers(pkg, workloads, ws2, args.rotate, dev)
+            ms2, _ = time_layers(pkg, l2, x, max(50, args.steps // 2), 10)
+            del l2
+            torch.cuda.empty_cache()
+            extras["tp2_share_m16"] = {"intermediate": ws2.intermediate, "us_per_layer": round(ms2 * 1e3, 2),
+                                       "gbs": round(ws2.algorithmic_bytes() / (ms2 / 1e3) / 1e9, 2),
+                                       "algorithmic_bytes_per_layer": ws2.algorithmic_bytes()}
             # 64-layer stack, chained through the residual stream
             _log("64-layer stack")
             stack = make_layers(pkg, workloads, wl, 64, dev, first_layer=100)

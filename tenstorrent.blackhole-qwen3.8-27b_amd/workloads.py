@@ -52,6 +52,10 @@ WORKLOADS = {
     "qwen3-27b-mlp-m1-bf4": Workload("qwen3-27b-mlp-m1-bf4", 5120, 17408, 1, "bf4", True),
     "qwen3-27b-mlp-m32-bf4": Workload("qwen3-27b-mlp-m32-bf4", 5120, 17408, 32, "bf4", True),
     "qwen3-27b-mlp-prefill-m2048-bf4": Workload("qwen3-27b-mlp-prefill-m2048-bf4", 5120, 17408, 2048, "bf4", False),
+    # one GPU's share of a layer split two ways along the intermediate dimension (the reference's
+    # TP2 shard: gate/up rows and down columns 8704 of 17408, docker/qwen-c2-graft/graft/mlp.py:49-151)
+    "qwen3-27b-tp2-share-m16-bfp8": Workload("qwen3-27b-tp2-share-m16-bfp8", 5120, 8704, 16, "bfp8", True),
+    "qwen3-27b-tp2-share-m16-bf4": Workload("qwen3-27b-tp2-share-m16-bf4", 5120, 8704, 16, "bf4", True),
 }
 
 
