@@ -76,8 +76,9 @@ struct GvTune {
   static constexpr int kQb = (NMAT == 2 ? 2 : 4) * MG;
 };
 
-// First superblock of K split q (split lengths differ by at most one superblock).
-__host__ __device__ inline int split_start(int q, int C, int S) { return (int)((long)q * C / S); }
+// First superblock of K split q (split lengths differ by at most one superblock).  q * C stays
+// far below 2^31 (C = K / 256 and q < S <= 16), so 32-bit arithmetic suffices.
+__host__ __device__ inline int split_start(int q, int C, int S) { return q * C / S; }
 
 // WF: 0 bf16, 1 bfp8, 2 bf4 weights.  A bf4 register holds two K-steps of the lane.
 template <int WF, int NMAT, int SPS>
@@ -408,6 +409,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
   __shared__ float s_ss[ROWS];
   __shared__ float s_sx[ROWS];
   __shared__ int s_last;
+  __shared__ int s_seg[NW][2];  // first and last tile of each wave's unit range (empty: 1 > -1)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int w = xcd_logical(blockIdx.x, p.P);
@@ -542,6 +544,10 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
     gn = __longlong_as_double((long long)p.tg->max_row_norm_bits);
     un = __longlong_as_double((long long)p.tu->max_row_norm_bits);
   }
+  if (lane == 0) {
+    s_seg[wave][0] = ua < ub ? ua / kq : 1;
+    s_seg[wave][1] = ua < ub ? (ub - 1) / kq : -1;
+  }
   __syncthreads();  // every wave is done with the staged activations: their LDS takes the slots
 
   // parked partials -> LDS slots (slot index = tile - the wave's first tile)
@@ -567,9 +573,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
       for (int mg = 0; mg < MG; ++mg) sum[mat][mg] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int v = 0; v < NW; ++v) {
-      const int va = (int)((long)v * U / NW), vb = (int)((long)(v + 1) * U / NW);
-      if (va >= vb) continue;
-      const int vt0 = va / kq, vt1 = (vb - 1) / kq;
+      const int vt0 = s_seg[v][0], vt1 = s_seg[v][1];
       if (tl < vt0 || tl > vt1) continue;
       const f32x4* slot = slots + (size_t)(v * p.maxseg + (tl - vt0)) * SLOT;
 #pragma unroll
