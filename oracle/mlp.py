@@ -87,3 +87,17 @@ def tolerance_ok(actual, expected, rel=1e-2):
     err = float(np.max(np.abs(actual - expected))) if expected.size else 0.0
     bound = rel * rms
     return err <= bound, err, bound
+
+
+def tolerance_ok_bf16(actual, expected, rel=1e-2):
+    """The same bar for an output rounded to bf16, which cannot be closer to the fp32 oracle than
+    its own rounding: elementwise ``|actual - expected| - half a bf16 ulp of expected <=
+    rel * RMS(expected)``.  Returns (ok, worst excess, bound)."""
+    actual = np.asarray(actual, dtype=np.float64)
+    expected = np.asarray(expected, dtype=np.float64)
+    rms = float(np.sqrt(np.mean(expected * expected)))
+    _, e = np.frexp(np.abs(expected))
+    half_ulp = np.ldexp(1.0, e - 9)  # |expected| in [2^(e-1), 2^e): bf16 ulp 2^(e-8)
+    worst = float((np.abs(actual - expected) - half_ulp).max()) if expected.size else 0.0
+    bound = rel * rms
+    return worst <= bound, worst, bound

@@ -414,6 +414,8 @@ class Qwen36MLP:
         if out is not None:
             if tuple(out.shape) != tuple(shape):
                 raise ValueError("out must have the activation's shape")
+            if not out.is_contiguous():  # a reshape would write into a copy
+                raise ValueError("out must be contiguous")
             o2d = out.reshape(M, shape[-1])
         y = mlp_forward(x2d, self.weights, residual=r2d, out=o2d, workspace=self._workspace_for(M),
                         out_dtype=out_dtype)
@@ -438,6 +440,8 @@ class Qwen36MLP:
         if out is not None:
             if tuple(out.shape) != tuple(shape):
                 raise ValueError("out must have h's shape")
+            if not out.is_contiguous():  # a reshape would write into a copy
+                raise ValueError("out must be contiguous")
             o2d = out.reshape(M, shape[-1])
         y = mlp_forward_rmsnorm(h2d, norm_weight, self.weights, eps=eps, out=o2d, workspace=self._workspace_for(M),
                                 out_dtype=out_dtype)

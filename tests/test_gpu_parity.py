@@ -51,15 +51,9 @@ def _check(y, ref, what):
 def _check_bf16(y, ref, what):
     """A bf16 output cannot be closer to the fp32 oracle than its own rounding: elementwise
     |y - ref| <= 1e-2 * RMS(ref) + half a bf16 ulp of ref."""
-    y = np.asarray(y, np.float64)
-    ref = np.asarray(ref, np.float64)
-    rms = float(np.sqrt(np.mean(ref * ref)))
-    _, e = np.frexp(np.abs(ref))
-    half_ulp = np.ldexp(1.0, e - 9)  # |ref| in [2^(e-1), 2^e): bf16 ulp 2^(e-8)
-    excess = np.abs(y - ref) - half_ulp
-    worst = float(excess.max())
-    print(f"{what} (bf16 out): max(|err| - half ulp)={worst:.4e} bar={TOL * rms:.4e}", flush=True)
-    assert worst <= TOL * rms, f"{what}: {worst} > {TOL * rms}"
+    ok, worst, bound = omlp.tolerance_ok_bf16(y, ref, TOL)
+    print(f"{what} (bf16 out): max(|err| - half ulp)={worst:.4e} bar={bound:.4e}", flush=True)
+    assert ok, f"{what}: {worst} > {bound}"
 
 
 # ---------------------------------------------------------------- load-time kernels (bit-exact)
@@ -343,6 +337,13 @@ def test_shape_errors(pkg, cuda):
         mlp.forward(torch.zeros((2, 1024), dtype=torch.bfloat16))
     with pytest.raises(ValueError):
         pkg.pack_weight(torch.zeros((17, 256), dtype=torch.bfloat16, device=cuda))
+    # an output that a reshape could only copy is refused (the result would land in the copy)
+    x = torch.zeros((2, 1024), dtype=torch.bfloat16, device=cuda)
+    strided = torch.zeros((1024, 2), dtype=torch.bfloat16, device=cuda).t()
+    with pytest.raises(ValueError):
+        mlp.forward(x, out=strided)
+    with pytest.raises(ValueError):
+        mlp.forward_rmsnorm(x, torch.zeros(1024, dtype=torch.bfloat16, device=cuda), out=strided)
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])

@@ -280,6 +280,24 @@ def test_tolerance_helper():
     assert not ok
 
 
+def test_tolerance_helper_bf16():
+    """The bf16 bar allows exactly half a bf16 ulp of the expected value on top of the fp32 bar:
+    at 5.0 (exponent range [4, 8), ulp 2^-5) a rounded output may sit 2^-6 away for free."""
+    exp = np.zeros(1000)
+    exp[0] = 5.0
+    bar = 1e-2 * 5.0 / math.sqrt(1000)  # 1.58e-3, below the half ulp 2^-6
+    err = np.zeros(1000)
+    err[0] = 2.0**-6
+    ok, worst, bound = omlp.tolerance_ok_bf16(exp + err, exp)
+    assert ok and abs(worst) < 1e-15 and abs(bound - bar) < 1e-12
+    err[0] = 2.0**-6 + bar * 1.01
+    ok, worst, _ = omlp.tolerance_ok_bf16(exp + err, exp)
+    assert not ok and abs(worst - bar * 1.01) < 1e-12
+    # the unrounded bar alone rejects the first case
+    err[0] = 2.0**-6
+    assert not omlp.tolerance_ok(exp + err, exp)[0]
+
+
 # ---------------------------------------------------------------- zero-centred RMSNorm prologue
 
 
