@@ -14,10 +14,10 @@
 // matrices of features by MG x 16 tokens; every A fragment feeds MG x 2 products and every B
 // fragment NMAT x TPW x 2.
 //
-// Pipeline per 64-K step s: issue the B loads of step s+3 and compute step s from LDS slot s%3
-// and register stage s%3; issue the weight loads of step s+3 into that stage; write the B rows of
-// step s+2 (loaded one step earlier) into slot (s+2)%3; one barrier.  Loads beyond the last step
-// are clamped duplicates, so every load is unconditional.
+// Pipeline per 64-K step s: compute step s from LDS slot s%3 and register stage s%3; issue the
+// weight loads of step s+3 into that stage; write the B rows of step s+2 (requested one or three
+// steps earlier, by the number of B register buffers) into slot (s+2)%3; one barrier.  Loads
+// beyond the last step are clamped duplicates, so every load is unconditional.
 //
 // Epilogue (fp32 accumulators in registers): gate/up -> h = silu(g) * u rounded once (fp16 *
 // 2^th for bfp8, bf16 for bf16 weights); down -> out = residual + y.  No cross-workgroup
@@ -48,7 +48,7 @@ struct TlStage {
   uint32_t e[NMAT][TPW];
 };
 
-template <int WF, int NMAT, int TPW, int MG, int NWV>
+template <int WF, int NMAT, int TPW, int MG, int NWV, int NBB>
 __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   constexpr int NT = NWV * 64;
   constexpr int SLOT = MG * 2048;      // LDS bytes of one 64-K step of B
@@ -166,41 +166,68 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
     }
   };
 
+  // B rows travel global -> registers -> LDS.  NBB = 3 register buffers give every B load three
+  // iterations to land (step s+5 is requested in iteration s, like the weight stages); NBB = 2
+  // gives one (step s+3 is requested at the top of iteration s) for the kernels whose occupancy
+  // the third buffer's registers would halve.
   TlStage<WF, NMAT, TPW> s0, s1, s2;
-  u32x4 bA[CPT], bB[CPT];
-  bload(bA, 0);
-  bload(bB, 1);
+  u32x4 b0[CPT], b1[CPT], b2[CPT];
+  bload(b0, 0);
+  bload(b1, 1);
   wload(s0, 0);
   wload(s1, 1);
   wload(s2, 2);
-  bstore(bA, 0);
-  bstore(bB, 1);
-  bload(bA, 2);
-  __syncthreads();
-  // iteration s: bnext receives step s+3 (it held step s+1, already in LDS); bwrite holds step
-  // s+2 and goes to slot (s+2) % 3, which was last read in iteration s-1.
-  auto iter = [&](TlStage<WF, NMAT, TPW>& cur, u32x4(&bnext)[CPT], u32x4(&bwrite)[CPT], int s) {
-    bload(bnext, s + 3);
-    compute(cur, s);
-    wload(cur, s + 3);
-    bstore(bwrite, s + 2);
-    __syncthreads();
-  };
+  bstore(b0, 0);
+  bstore(b1, 1);
+  bload(b2, 2);
   int s = 0;
-  for (; s + 6 <= nst; s += 6) {
-    iter(s0, bB, bA, s);
-    iter(s1, bA, bB, s + 1);
-    iter(s2, bB, bA, s + 2);
-    iter(s0, bA, bB, s + 3);
-    iter(s1, bB, bA, s + 4);
-    iter(s2, bA, bB, s + 5);
+  if constexpr (NBB == 3) {
+    bload(b0, 3);
+    bload(b1, 4);
+    __syncthreads();
+    // iteration s: the buffer holding step s+2 goes to LDS slot (s+2) % 3 (last read in
+    // iteration s-1) and then receives step s+5.
+    auto iter = [&](TlStage<WF, NMAT, TPW>& cur, u32x4(&bw)[CPT], int s) {
+      compute(cur, s);
+      wload(cur, s + 3);
+      bstore(bw, s + 2);
+      bload(bw, s + 5);
+      __syncthreads();
+    };
+    for (; s + 3 <= nst; s += 3) {
+      iter(s0, b2, s);
+      iter(s1, b0, s + 1);
+      iter(s2, b1, s + 2);
+    }
+    const int r = nst - s;
+    if (r > 0) iter(s0, b2, s);
+    if (r > 1) iter(s1, b0, s + 1);
+  } else {
+    __syncthreads();
+    // iteration s: bnext receives step s+3 (it held step s+1, already in LDS); bwrite holds step
+    // s+2 and goes to slot (s+2) % 3, which was last read in iteration s-1.
+    auto iter = [&](TlStage<WF, NMAT, TPW>& cur, u32x4(&bnext)[CPT], u32x4(&bwrite)[CPT], int s) {
+      bload(bnext, s + 3);
+      compute(cur, s);
+      wload(cur, s + 3);
+      bstore(bwrite, s + 2);
+      __syncthreads();
+    };
+    for (; s + 6 <= nst; s += 6) {
+      iter(s0, b1, b2, s);
+      iter(s1, b2, b1, s + 1);
+      iter(s2, b1, b2, s + 2);
+      iter(s0, b2, b1, s + 3);
+      iter(s1, b1, b2, s + 4);
+      iter(s2, b2, b1, s + 5);
+    }
+    const int r = nst - s;
+    if (r > 0) iter(s0, b1, b2, s);
+    if (r > 1) iter(s1, b2, b1, s + 1);
+    if (r > 2) iter(s2, b1, b2, s + 2);
+    if (r > 3) iter(s0, b2, b1, s + 3);
+    if (r > 4) iter(s1, b1, b2, s + 4);
   }
-  const int r = nst - s;
-  if (r > 0) iter(s0, bB, bA, s);
-  if (r > 1) iter(s1, bA, bB, s + 1);
-  if (r > 2) iter(s2, bB, bA, s + 2);
-  if (r > 3) iter(s0, bA, bB, s + 3);
-  if (r > 4) iter(s1, bB, bA, s + 4);
 
   // epilogue: lane l holds features 4 * (l / 16) + v of each tile for token l % 16 of each group
   const int col = lane & 15, rq = (lane >> 4) * 4;
@@ -267,16 +294,19 @@ constexpr int kTlNWV = 8;  // waves per block
 //            block): every dequantised weight fragment feeds 16 products (686-696 us, against
 //            782-791 us for 2 tiles x 4 groups);
 //   down:    2 tiles per wave x 4 groups (256 features x 64 tokens): 415-423 us, against 535-542
-//            us for 1 tile x 8 groups.
+//            us for 1 tile x 8 groups, 488-492 us for 4 tiles x 4 groups, 424-437 us for 5.
+// B register buffers (NBB): 3 where the registers allow two blocks per CU anyway or one block
+// regardless (gate/up bfp8 704-707 us against 711-723; bf16 down 445 against 514 us); 2 for the
+// bfp8 down projection, which keeps two blocks per CU only under 128 VGPRs (420 against 519 us).
 constexpr int kTlGuTPW = 1, kTlGuMG = 8;
 constexpr int kTlDnTPW = 2, kTlDnMG = 4;
 
-template <int WF, int NMAT, int TPW, int MG>
+template <int WF, int NMAT, int TPW, int MG, int NBB>
 static int launch_tiled(TlParams p, hipStream_t s) {
   const int nbn = p.N / (kTlNWV * TPW * kTileRows);
   p.nbm = (p.M + MG * 16 - 1) / (MG * 16);
   const size_t lds = (size_t)3 * MG * 2048;
-  launch_timed(NMAT == 2 ? 0 : 1, tiled_kernel<WF, NMAT, TPW, MG, kTlNWV>, dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s,
+  launch_timed(NMAT == 2 ? 0 : 1, tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s,
                p);
   return check_launch("tiled_kernel");
 }
@@ -312,9 +342,9 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.tout = th;
   g.out = h;
   constexpr int GT = kTlGuTPW, GM = kTlGuMG, DT = kTlDnTPW, DM = kTlDnMG;
-  int rc = fmt == 2   ? launch_tiled<2, 2, GT, GM>(g, s)
-           : fmt == 1 ? launch_tiled<1, 2, GT, GM>(g, s)
-                      : launch_tiled<0, 2, GT, GM>(g, s);
+  int rc = fmt == 2   ? launch_tiled<2, 2, GT, GM, 3>(g, s)
+           : fmt == 1 ? launch_tiled<1, 2, GT, GM, 3>(g, s)
+                      : launch_tiled<0, 2, GT, GM, 2>(g, s);
   if (rc) return rc;
   TlParams d{};
   d.w0 = a.wd;
@@ -330,7 +360,7 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.residual = a.residual;
   d.out_f32 = a.out_f32;
   d.res_f32 = a.res_f32;
-  rc = dfmt == 1 ? launch_tiled<1, 1, DT, DM>(d, s) : launch_tiled<0, 1, DT, DM>(d, s);
+  rc = dfmt == 1 ? launch_tiled<1, 1, DT, DM, 2>(d, s) : launch_tiled<0, 1, DT, DM, 3>(d, s);
   if (rc) return rc;
   return 0;
 }
