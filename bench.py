@@ -250,6 +250,13 @@ def main():
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": gu_bytes},
     }
+    if wl.tokens > 32:  # many-token chunks run the matrix-core kernels: bound by the MFMA peak
+        gu_flops = 4 * wl.tokens * wl.hidden * wl.intermediate
+        gu_tf = gu_flops / (gu_ms / 1e3) / 1e12
+        result["roofline"] = {"kernel": "gate/up projection (tiled_kernel, 2 matrices)", "bound": "mfma",
+                              "achieved": round(gu_tf, 1), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(gu_tf / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                              "algorithmic_flops_per_launch": gu_flops}
     del layers
     torch.cuda.empty_cache()
     if not args.no_extras:
@@ -319,7 +326,7 @@ def main():
             wp = workloads.WORKLOADS["qwen3-27b-mlp-prefill-m2048-bfp8"]
             lp = make_layers(pkg, workloads, wp, 2, dev)
             xp = workloads.activations(wp.tokens, wp.hidden, gain=False, device=dev)
-            msp, _ = time_layers(pkg, lp, xp, 10, 2)
+            msp, _ = time_layers(pkg, lp, xp, 20, 5)
             tflops = wp.flops() / (msp / 1e3) / 1e12
             extras["prefill_m2048"] = {"us_per_layer": round(msp * 1e3, 1), "tflops": round(tflops, 1),
                                        "mfma_util_vs_bf16_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
