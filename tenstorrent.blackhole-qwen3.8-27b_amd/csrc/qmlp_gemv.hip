@@ -67,6 +67,9 @@ struct GvParams {
 
 constexpr int kPssStride = 64;  // floats of token sums per workgroup
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 // Per-(matrices, token groups) constants.  Both bound the registers of one wave to ~48 VGPRs:
 //   kMaxSeg: parked partial tiles per wave (the planner rejects splits that need more);
 //   kQb:     K splits whose partials the last arrival requests in its first batch.
@@ -134,6 +137,54 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, int kq, const 
 #pragma unroll
     for (int c = 0; c < MAXCH; ++c)
       if (c < nch) *(u32x4*)(ldsb + lds_off((tl + c * TPR) * 8)) = bs.v[c];
+    return;
+  }
+  if constexpr (!NORM) {
+    // bf16 x -> fp16 * 2^t on packed 16-bit words: the magnitudes' integer maximum is the
+    // maximum value, the sum of squares comes from v_dot2_f32_bf16, and the conversion is
+    // fp16 bits = ((|x| bits - ((112 - t) << 7)) << 3) | sign, exact while x * 2^t is a normal
+    // half; values below 2^-14 after scaling (2^-28 of the range maximum) are flushed to zero.
+    u16x2 mx2 = {0, 0};
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < MAXCH; ++c)
+      if (c < nch)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t r = bs.v[c][i];
+          mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(u16x2, r & 0x7fff7fffu));
+          ss = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, r), __builtin_bit_cast(bf16x2, r), ss, false);
+        }
+    uint32_t mb = max((uint32_t)mx2.x, (uint32_t)mx2.y);
+#pragma unroll
+    for (int o = TPR / 2; o > 0; o >>= 1) {
+      mb = max(mb, (uint32_t)__shfl_xor((int)mb, o));
+      ss += __shfl_xor(ss, o);
+    }
+    const float mxf = bf16_to_f32((uint16_t)mb);
+    int e2 = 0;
+    if (mxf > 0.f) frexpf(mxf, &e2);
+    const int t = mxf > 0.f ? min(15 - e2, 112) : 0;
+    if (tl == 0) {
+      lds_t[m] = t;
+      lds_ss[m] = ss;
+      lds_sx[m] = 0.f;
+    }
+    const uint32_t dd = (uint32_t)(112 - t) << 7;
+    const u16x2 d2 = __builtin_bit_cast(u16x2, dd | (dd << 16));
+#pragma unroll
+    for (int c = 0; c < MAXCH; ++c) {
+      if (c < nch) {
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t r = bs.v[c][i];
+          const u16x2 sub = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, r & 0x7fff7fffu), d2);
+          o[i] = __builtin_bit_cast(uint32_t, (u16x2)(sub << (u16x2){3, 3})) | (r & 0x80008000u);
+        }
+        *(u32x4*)(ldsb + lds_off((tl + c * TPR) * 8)) = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
     return;
   }
   auto value = [&](int c, int i, int hi, float& xr) {
