@@ -347,10 +347,11 @@ def test_shape_errors(pkg, cuda):
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
-@pytest.mark.parametrize("H,I,M", [(1024, 3072, 2048), (5120, 17408, 256), (1024, 3072, 200)])
+@pytest.mark.parametrize("H,I,M", [(1024, 3072, 2048), (5120, 17408, 256), (1024, 3072, 200), (1024, 3072, 33)])
 def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
     """Many-token forwards (the LDS-tiled matrix-core kernels): a full 2048-token chunk, the 27B
-    shape, and a token count that leaves a partial token block."""
+    shape, a token count that leaves a partial token block, and the narrowest width that takes
+    this path (one partial block in each projection)."""
     import torch
     from qwen_mlp_amd import workloads
 
