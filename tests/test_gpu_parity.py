@@ -217,6 +217,33 @@ def test_forward_every_small_width(pkg, cuda, fmt):
         _check(y.cpu().numpy(), _oracle(xf, hw), f"{fmt} H={H} I={I} M={M}")
 
 
+def test_forward_random_shapes(pkg, cuda):
+    """Seeded irregular shapes (odd superblock and tile counts, every dispatch width, every format)
+    against the oracle, fp32 and bf16 outputs."""
+    import numpy as np
+    import torch
+    from qwen_mlp_amd import workloads
+
+    rng = np.random.default_rng(20261201)
+    Hs, Is = [256, 768, 1280, 2304, 4352], [256, 1280, 2816, 4864, 6400]
+    Ms = [1, 3, 8, 15, 16, 17, 24, 31, 32, 33, 40, 64, 96, 130]
+    for case in range(18):
+        H, I = int(rng.choice(Hs)), int(rng.choice(Is))
+        M, fmt = int(rng.choice(Ms)), str(rng.choice(["bf16", "bfp8", "bf4"]))
+        print(f"case random {case}: {fmt} H={H} I={I} M={M}", flush=True)
+        sd = workloads.state_dict(H, I, layer=30 + case, device=cuda)
+        mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=M)
+        x = workloads.activations(M, H, seed=7391 + case, device=cuda)
+        y32 = mlp.forward(x, residual=x, out_dtype=torch.float32)
+        y16 = mlp.forward(x, residual=x)
+        torch.cuda.synchronize()
+        ref = _oracle(x.float().cpu().numpy(), _host_weights(pkg, sd, fmt))
+        _check(y32.cpu().numpy(), ref, f"random {case} {fmt} H={H} I={I} M={M}")
+        _check_bf16(y16.float().cpu().numpy(), ref, f"random {case} {fmt} H={H} I={I} M={M}")
+        del mlp, sd
+        torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8"])
 def test_forward_stream_fallback(pkg, cuda, fmt):
     """A down projection too long for the split kernel's staged activations (K = 76800 > 16 splits
