@@ -10,7 +10,7 @@ This package restates, on the CPU, the arithmetic the GPU library must reproduce
   the quantiser, dequantiser and SwiGLU used to cross-check the numpy code.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import
-this package, and only as the checker.  The product (the HIP library and its Python host module)
+this package, and only to check results against.  The product (the HIP library and its Python host module)
 never routes through it; it fails loudly when its native extension is missing.
 
 Pinning (what checks each function, see ``tests/test_oracle.py``):
