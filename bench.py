@@ -195,7 +195,7 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: this build runs the unsharded MLP on a single MI355X; "
+        print("bench.py measures one GPU: the library runs the unsharded MLP on a single MI355X; "
               f"--gpus {args.gpus} (WORLD_SIZE={world}) is not supported.", file=sys.stderr)
         sys.exit(2)
     import torch

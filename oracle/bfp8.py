@@ -17,8 +17,8 @@ non-zero values of the group (so every ``|v| < 2**E``); the scale is ``2**(E - 7
 This is the block-float rule of the reference's BF8_b check, ``bf8_exact``
 (``scripts/ci/ordered_cache_hw_plan.py:243-260``): a group is exact when
 ``v * 2**(7 - shared) `` is an integer of magnitude below 2**7.  The reference groups 16 values
-along the tile row (``BF8_GROUP = 16``, ``ordered_cache_hw_plan.py:25``); this build groups them
-along K so that one 16-byte load holds one group.
+along the tile row (``BF8_GROUP = 16``, ``ordered_cache_hw_plan.py:25``); the GPU library groups
+them along K so that one 16-byte load holds one group.
 
 Device ("tiled") format
 -----------------------

@@ -215,3 +215,16 @@ def test_pack_checkpoint_finds_mlp_weights(tmp_path, pkg):
     assert pc.parse_layers("0", found) == [0] and pc.parse_layers(None, found) == [0, 3]
     with pytest.raises(ValueError):
         pc.parse_layers("0-2", found)
+
+
+def test_bench_refuses_several_gpus():
+    """bench.py measures one GPU; asking for more exits with a message and status 2 before any
+    GPU work."""
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
