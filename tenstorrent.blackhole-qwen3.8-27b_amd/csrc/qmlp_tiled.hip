@@ -285,6 +285,244 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   }
 }
 
+// ---------------------------------------------------------------- 32 x 32 gate/up variant
+//
+// Dispatched for bf4 weights (the format where it measures faster); the bf16 and bfp8 branches
+// are kept so that the variant stays comparable across formats.
+//
+// Same formulation and pipeline as tiled_kernel (gate/up only), on 32x32x16 matrix-core products:
+// each wave owns the 32-row feature pair (tiles 2 P and 2 P + 1) of both matrices for MG groups of
+// 32 tokens.  Every 1 KB B fragment read from LDS then feeds two 32x32 products (65536 flops)
+// instead of two 16x16 ones, and the wave issues half the matrix-core instructions, while every
+// dequantised weight value still feeds MG x 32 tokens.
+//
+// A operand from the packed layout as it stands: lane l = 32 hk + 16 ts + r takes row r of tile
+// 2 P + ts and the packed chunks q = 2 hk and 2 hk + 1 of each K-step (K = 64 j + 32 hk + 0..31),
+// i.e. the 16-byte slots of packed lanes 32 hk + r and 32 hk + 16 + r.  Product u (0..3) of the
+// step takes the lane's values 8 u .. 8 u + 7 of those 32: K = 64 j + 32 hk + 8 u + (0..7) on the
+// lanes whose A index half is hk.  The B fragment of product u therefore holds, in lane
+// l = 32 hk + c, the K values 64 j + 32 hk + 8 u + (0..7) of token c of the group.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// 16-byte LDS slot of product u's B fragment for lane l inside one group's 4 KB step image.  The
+// 8 lanes 8a..8a+7 of a fragment read one aligned 128-byte run (a rotation of it), and the 8 slots
+// one token row writes per step (all (u, hk) pairs) fall on distinct 16-byte bank groups.
+__host__ __device__ inline uint32_t b32_slot(int u, int l) {
+  return (uint32_t)(u * 64 + (l & ~7) + ((l + 2 * u + (l >> 5)) & 7));
+}
+
+template <int WF>
+struct Tl32Stage {
+  typename StepWord<WF>::type w[2][WF ? 2 : 4];
+  uint32_t e[2][2];
+};
+
+template <int WF, int MG, int NBB>
+__global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
+  constexpr int NWV = 8, NT = NWV * 64;
+  constexpr int SLOT = MG * 4096;     // LDS bytes of one 64-K step of B
+  constexpr int CPT = MG * 256 / NT;  // 16-byte B chunks per thread per step
+  static_assert(CPT * NT == MG * 256, "B chunks must divide evenly over the threads");
+  constexpr int BLK = WF == 2 ? kBf4Block : (WF ? kBfp8Block : kBf16Block);
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int L = xcd_logical(blockIdx.x, gridDim.x);  // blocks sharing weights share an XCD
+  const int bn = L / p.nbm, bm = L % p.nbm;
+  const int m0 = bm * MG * 32;
+  const int pair = bn * NWV + wave;
+  const int nst = p.C * kSteps;
+
+  // B chunk c = threadIdx.x + i * NT: token row r = c / 8, K values 8 k8 .. 8 k8 + 7 of the step
+  // (k8 = c % 8 = 4 hk + u).  Rows beyond M repeat row M - 1 (their outputs are not stored).
+  uint32_t goff[CPT], loff[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = threadIdx.x + i * NT, r = c >> 3, k8 = c & 7;
+    const int mr = min(m0 + r, p.M - 1);
+    goff[i] = (uint32_t)(mr * p.K + k8 * 8) * 2u;
+    loff[i] = (uint32_t)(r >> 5) * 4096u + b32_slot(k8 & 3, 32 * (k8 >> 2) + (r & 31)) * 16u;
+  }
+  const uint8_t* srcb = (const uint8_t*)p.src;
+  auto bload = [&](u32x4(&v)[CPT], int step) {
+    const uint8_t* base = srcb + (size_t)min(step, nst - 1) * 128;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) v[i] = *(const u32x4*)(base + goff[i]);
+  };
+  auto bstore = [&](const u32x4(&v)[CPT], int step) {
+    uint8_t* slot = lds + (step % 3) * SLOT;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) *(u32x4*)(slot + loff[i]) = v[i];
+  };
+
+  const int hk = lane >> 5;
+  const uint8_t* wt[2];
+#pragma unroll
+  for (int mat = 0; mat < 2; ++mat)
+    wt[mat] = (mat ? p.w1 : p.w0) + (size_t)(2 * pair + ((lane >> 4) & 1)) * p.C * BLK;
+  const uint32_t lp0 = (uint32_t)(32 * hk + (lane & 15)), lp1 = lp0 + 16u;
+  auto wload = [&](Tl32Stage<WF>& st, int step) {
+    const int sc = min(step, nst - 1);
+    const uint32_t bo = (uint32_t)(sc >> 2) * BLK;
+#pragma unroll
+    for (int mat = 0; mat < 2; ++mat) {
+      const uint8_t* b = wt[mat] + bo;
+      if constexpr (WF == 1) {
+        st.w[mat][0] = *(const u32x4*)(b + (sc & 3) * 1024 + lp0 * 16u);
+        st.w[mat][1] = *(const u32x4*)(b + (sc & 3) * 1024 + lp1 * 16u);
+        st.e[mat][0] = *(const uint32_t*)(b + 4096 + lp0 * 4u);
+        st.e[mat][1] = *(const uint32_t*)(b + 4096 + lp1 * 4u);
+      } else if constexpr (WF == 2) {
+        const uint32_t o = (uint32_t)(sc & 2) * 512u + (uint32_t)(sc & 1) * 8u;
+        st.w[mat][0] = *(const u32x2*)(b + o + lp0 * 16u);
+        st.w[mat][1] = *(const u32x2*)(b + o + lp1 * 16u);
+        st.e[mat][0] = *(const uint32_t*)(b + 2048 + lp0 * 4u);
+        st.e[mat][1] = *(const uint32_t*)(b + 2048 + lp1 * 4u);
+      } else {
+        const uint8_t* bb = b + (sc & 3) * 2048;
+        st.w[mat][0] = *(const u32x4*)(bb + lp0 * 16u);
+        st.w[mat][1] = *(const u32x4*)(bb + 1024 + lp0 * 16u);
+        st.w[mat][2] = *(const u32x4*)(bb + lp1 * 16u);
+        st.w[mat][3] = *(const u32x4*)(bb + 1024 + lp1 * 16u);
+      }
+    }
+  };
+
+  f32x16 acc[2][MG];
+#pragma unroll
+  for (int mat = 0; mat < 2; ++mat)
+#pragma unroll
+    for (int g = 0; g < MG; ++g)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mat][g][v] = 0.f;
+
+  uint32_t bs[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) bs[u] = b32_slot(u, lane) * 16u;
+  auto compute = [&](const Tl32Stage<WF>& st, int step) {
+    const uint8_t* slot = lds + (step % 3) * SLOT;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      if constexpr (WF) {
+        f16x8 a[2][2];
+#pragma unroll
+        for (int mat = 0; mat < 2; ++mat) {
+          if constexpr (WF == 2)
+            dq16_bf4(st.w[mat][c].x, st.w[mat][c].y, scale_pair(st.e[mat][c], step & 3), a[mat][0], a[mat][1]);
+          else
+            dq16(st.w[mat][c], scale_pair(st.e[mat][c], step & 3), a[mat][0], a[mat][1]);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int g = 0; g < MG; ++g) {
+            const f16x8 b = __builtin_bit_cast(f16x8, *(const u32x4*)(slot + g * 4096 + bs[2 * c + h]));
+#pragma unroll
+            for (int mat = 0; mat < 2; ++mat)
+              acc[mat][g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mat][h], b, acc[mat][g], 0, 0, 0);
+          }
+      } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int g = 0; g < MG; ++g) {
+            const bf16x8 b = __builtin_bit_cast(bf16x8, *(const u32x4*)(slot + g * 4096 + bs[2 * c + h]));
+#pragma unroll
+            for (int mat = 0; mat < 2; ++mat)
+              acc[mat][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, st.w[mat][2 * c + h]),
+                                                                    b, acc[mat][g], 0, 0, 0);
+          }
+      }
+    }
+  };
+
+  // The pipeline of tiled_kernel: NBB = 3 B register buffers request step s+5 in iteration s,
+  // NBB = 2 request step s+3 at the top of iteration s; weights of step s+3 are requested right
+  // after step s's products; one barrier per step.
+  Tl32Stage<WF> s0, s1, s2;
+  u32x4 b0[CPT], b1[CPT], b2[CPT];
+  bload(b0, 0);
+  bload(b1, 1);
+  wload(s0, 0);
+  wload(s1, 1);
+  wload(s2, 2);
+  bstore(b0, 0);
+  bstore(b1, 1);
+  bload(b2, 2);
+  int s = 0;
+  if constexpr (NBB == 3) {
+    bload(b0, 3);
+    bload(b1, 4);
+    __syncthreads();
+    auto iter = [&](Tl32Stage<WF>& cur, u32x4(&bw)[CPT], int s) {
+      compute(cur, s);
+      wload(cur, s + 3);
+      bstore(bw, s + 2);
+      bload(bw, s + 5);
+      __syncthreads();
+    };
+    for (; s + 3 <= nst; s += 3) {
+      iter(s0, b2, s);
+      iter(s1, b0, s + 1);
+      iter(s2, b1, s + 2);
+    }
+    const int r = nst - s;
+    if (r > 0) iter(s0, b2, s);
+    if (r > 1) iter(s1, b0, s + 1);
+  } else {
+    __syncthreads();
+    auto iter = [&](Tl32Stage<WF>& cur, u32x4(&bnext)[CPT], u32x4(&bwrite)[CPT], int s) {
+      bload(bnext, s + 3);
+      compute(cur, s);
+      wload(cur, s + 3);
+      bstore(bwrite, s + 2);
+      __syncthreads();
+    };
+    for (; s + 6 <= nst; s += 6) {
+      iter(s0, b1, b2, s);
+      iter(s1, b2, b1, s + 1);
+      iter(s2, b1, b2, s + 2);
+      iter(s0, b2, b1, s + 3);
+      iter(s1, b1, b2, s + 4);
+      iter(s2, b2, b1, s + 5);
+    }
+    const int r = nst - s;
+    if (r > 0) iter(s0, b1, b2, s);
+    if (r > 1) iter(s1, b2, b1, s + 1);
+    if (r > 2) iter(s2, b1, b2, s + 2);
+    if (r > 3) iter(s0, b2, b1, s + 3);
+    if (r > 4) iter(s1, b1, b2, s + 4);
+  }
+
+  // epilogue: accumulator v of lane l holds feature 8 (v / 4) + 4 (l / 32) + v % 4 of the pair
+  // for token l % 32 of each group
+  const int col = lane & 31, rq = (lane >> 5) * 4;
+#pragma unroll
+  for (int g = 0; g < MG; ++g) {
+    const int m = m0 + g * 32 + col;
+    if (m >= p.M) continue;
+    const int ts = WF ? p.tsrc[m] : 0;
+    const int to = WF ? p.tout[m] : 0;
+#pragma unroll
+    for (int vq = 0; vq < 4; ++vq) {
+      const int n = pair * 32 + vq * 8 + rq;
+      uint16_t o[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        float gv = acc[0][g][4 * vq + v], uv = acc[1][g][4 * vq + v];
+        if constexpr (WF) {
+          gv = __builtin_amdgcn_ldexpf(gv, p.rowexp0[n + v] - ts);
+          uv = __builtin_amdgcn_ldexpf(uv, p.rowexp1[n + v] - ts);
+        }
+        const float hv = gv / (1.0f + expf(-gv)) * uv;
+        o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(hv, to)) : f32_to_bf16(hv);
+      }
+      *(u32x2*)((uint16_t*)p.out + (size_t)m * p.N + n) =
+          u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+    }
+  }
+}
+
 // ---------------------------------------------------------------- host side
 
 constexpr int kTlNWV = 8;  // waves per block
@@ -309,6 +547,21 @@ static int launch_tiled(TlParams p, hipStream_t s) {
   launch_timed(NMAT == 2 ? 0 : 1, tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s,
                p);
   return check_launch("tiled_kernel");
+}
+
+// 32 x 32 gate/up kernel (bf4 weights): 8 waves x 32 features x 4 groups of 32 tokens per
+// block.  It takes bf4 gate/up from 711-715 to 676-678 us at 2048 tokens; with bfp8 weights its
+// 256 VGPRs serialise the LDS reads (749 against 709-714 us) and bf16 spills (846-857 us), and a
+// two-stage weight pipeline that frees the registers only draws level (744-752 against 739-751).
+constexpr int kTl32MG = 4;
+
+template <int WF, int MG, int NBB>
+static int launch_tiled32(TlParams p, hipStream_t s) {
+  const int nbn = p.N / (kTlNWV * 2 * kTileRows);
+  p.nbm = (p.M + MG * 32 - 1) / (MG * 32);
+  const size_t lds = (size_t)3 * MG * 4096;
+  launch_timed(0, tiled32_kernel<WF, MG, NBB>, dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s, p);
+  return check_launch("tiled32_kernel");
 }
 
 bool tiled_supported(int M, int H, int I) {
@@ -342,7 +595,7 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.tout = th;
   g.out = h;
   constexpr int GT = kTlGuTPW, GM = kTlGuMG, DT = kTlDnTPW, DM = kTlDnMG;
-  int rc = fmt == 2   ? launch_tiled<2, 2, GT, GM, 3>(g, s)
+  int rc = fmt == 2   ? launch_tiled32<2, kTl32MG, 3>(g, s)
            : fmt == 1 ? launch_tiled<1, 2, GT, GM, 3>(g, s)
                       : launch_tiled<0, 2, GT, GM, 2>(g, s);
   if (rc) return rc;
