@@ -253,7 +253,8 @@ def main():
     if wl.tokens > 32:  # many-token chunks run the matrix-core kernels: bound by the MFMA peak
         gu_flops = 4 * wl.tokens * wl.hidden * wl.intermediate
         gu_tf = gu_flops / (gu_ms / 1e3) / 1e12
-        result["roofline"] = {"kernel": "gate/up projection (tiled_kernel, 2 matrices)", "bound": "mfma",
+        kname = "tiled_kernel" if wl.fmt == "bf16" else "tiled32_kernel"
+        result["roofline"] = {"kernel": f"gate/up projection ({kname}, 2 matrices)", "bound": "mfma",
                               "achieved": round(gu_tf, 1), "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                               "frac": round(gu_tf / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
                               "algorithmic_flops_per_launch": gu_flops}

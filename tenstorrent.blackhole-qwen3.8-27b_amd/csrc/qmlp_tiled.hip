@@ -287,8 +287,8 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
 
 // ---------------------------------------------------------------- 32 x 32 gate/up variant
 //
-// Dispatched for bf4 weights (the format where it measures faster); the bf16 and bfp8 branches
-// are kept so that the variant stays comparable across formats.
+// Dispatched for the block-float formats; the bf16 branch is kept so that the variant stays
+// comparable across formats.
 //
 // Same formulation and pipeline as tiled_kernel (gate/up only), on 32x32x16 matrix-core products:
 // each wave owns the 32-row feature pair (tiles 2 P and 2 P + 1) of both matrices for MG groups of
@@ -474,6 +474,9 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     auto iter = [&](Tl32Stage<WF>& cur, u32x4(&bnext)[CPT], u32x4(&bwrite)[CPT], int s) {
       bload(bnext, s + 3);
       compute(cur, s);
+      // keeps the next weight loads behind the products: hoisted above them, their registers
+      // make the compiler wait for every LDS read before its two products
+      __builtin_amdgcn_sched_barrier(0);
       wload(cur, s + 3);
       bstore(bwrite, s + 2);
       __syncthreads();
@@ -549,10 +552,10 @@ static int launch_tiled(TlParams p, hipStream_t s) {
   return check_launch("tiled_kernel");
 }
 
-// 32 x 32 gate/up kernel (bf4 weights): 8 waves x 32 features x 4 groups of 32 tokens per
-// block.  It takes bf4 gate/up from 711-715 to 676-678 us at 2048 tokens; with bfp8 weights its
-// 256 VGPRs serialise the LDS reads (749 against 709-714 us) and bf16 spills (846-857 us), and a
-// two-stage weight pipeline that frees the registers only draws level (744-752 against 739-751).
+// 32 x 32 gate/up kernel (block-float weights): 8 waves x 32 features x 4 groups of 32 tokens per
+// block.  At 2048 tokens: bf4 (three B buffers) 676-692 against 711-739 us for tiled_kernel; bfp8
+// (two B buffers, the next weight loads fenced behind the products) 721-723 against 732-737 us.
+// bf16 weights stay on tiled_kernel (846-857 us here: the A stages spill).
 constexpr int kTl32MG = 4;
 
 template <int WF, int MG, int NBB>
@@ -596,7 +599,7 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.out = h;
   constexpr int GT = kTlGuTPW, GM = kTlGuMG, DT = kTlDnTPW, DM = kTlDnMG;
   int rc = fmt == 2   ? launch_tiled32<2, kTl32MG, 3>(g, s)
-           : fmt == 1 ? launch_tiled<1, 2, GT, GM, 3>(g, s)
+           : fmt == 1 ? launch_tiled32<1, kTl32MG, 2>(g, s)
                       : launch_tiled<0, 2, GT, GM, 2>(g, s);
   if (rc) return rc;
   TlParams d{};
