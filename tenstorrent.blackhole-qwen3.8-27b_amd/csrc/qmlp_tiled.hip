@@ -9,9 +9,9 @@
 // each wave owns TPW 16-row tiles of each matrix and streams them through registers in the packed
 // layout (bfp8 and bf4 dequantised exactly to fp16 in registers, bf16 used as is).  The tokens are the
 // B operand: a block stages MG groups of 16 token rows, one 64-K step at a time, into a 3-slot LDS
-// ring shared by all its waves (bfrag_off's order, the same as the
-// weight-streaming kernels', so each lane reads its B fragment with two 16-byte LDS loads).  One block = NWV waves x TPW tiles x NMAT
-// matrices of features by MG x 16 tokens; every A fragment feeds MG x 2 products and every B
+// ring shared by all its waves (bfrag_off's order, the same as the weight-streaming kernels', so
+// each lane reads its B fragment with two 16-byte LDS loads).  One block = NWV waves x TPW tiles x
+// NMAT matrices of features by MG x 16 tokens; every A fragment feeds MG x 2 products and every B
 // fragment NMAT x TPW x 2.
 //
 // Pipeline per 64-K step s: compute step s from LDS slot s%3 and register stage s%3; issue the
