@@ -118,11 +118,32 @@ def copy_calibration(mib, device):
     del a, b
 
 
+# The sources that decide what the M <= 32 gate/up kernel reads and writes: a traffic figure
+# measured on other sources describes another kernel.
+TRAFFIC_SOURCES = ("qmlp_gemv.hip", "qmlp_common.h", "qmlp_internal.h", "qmlp_abi.hip")
+
+
+def kernel_source_hash():
+    """sha256 (first 16 hex digits) over the gate/up kernel's sources, in TRAFFIC_SOURCES order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "tenstorrent.blackhole-qwen3.8-27b_amd", "csrc")
+    for name in TRAFFIC_SOURCES:
+        with open(os.path.join(csrc, name), "rb") as f:
+            h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
 def read_traffic(workload):
-    """HBM bytes per launch of the gate/up kernel from the committed counter summary (or None)."""
+    """HBM bytes per launch of the gate/up kernel from the committed counter summary.
+
+    Returns (bytes or None, note).  The summary is used only when it names this workload and was
+    measured on the current kernel sources (its ``kernel_source_sha256`` line); otherwise the bench
+    line reports no traffic rather than a stale figure."""
     path = os.path.join(ROOT, "profiles", "gemv_gate_up_m16_bfp8_traffic.md")
     if not os.path.exists(path):
-        return None
+        return None, "no counter summary"
     vals = {}
     with open(path) as f:
         for line in f:
@@ -130,11 +151,13 @@ def read_traffic(workload):
                 k, v = line[2:].split(":", 1)
                 vals[k.strip()] = v.strip().strip("`")
     if vals.get("workload") != workload:
-        return None
+        return None, f"counter summary is for {vals.get('workload')}"
+    if vals.get("kernel_source_sha256") != kernel_source_hash():
+        return None, "counter summary was measured on other kernel sources"
     try:
-        return int(vals["hbm_bytes_per_launch"])
+        return int(vals["hbm_bytes_per_launch"]), "profiles/gemv_gate_up_m16_bfp8_traffic.md"
     except (KeyError, ValueError):
-        return None
+        return None, "counter summary has no byte count"
 
 
 def cpu_baseline(pkg, workloads, wl, device, seconds):
@@ -148,7 +171,8 @@ def cpu_baseline(pkg, workloads, wl, device, seconds):
     from oracle import bfp8 as obfp8
     from oracle import mlp as omlp
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    # every core this process may run on (os.cpu_count() unless an affinity mask narrows it)
+    threads = max(1, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1))
     torch.set_num_threads(threads)
     sd = workloads.state_dict(wl.hidden, wl.intermediate, layer=0, device=device)
     w = {}
@@ -186,7 +210,8 @@ def cpu_baseline(pkg, workloads, wl, device, seconds):
         "cores": threads,
         "kind": "port",
         "sample": f"{len(times)} single-layer forwards of the same workload (median), torch fp32 on "
-                  f"dequantised weights, {threads} threads, os.cpu_count()={os.cpu_count()}, {cpu_model}",
+                  f"dequantised weights, {threads} threads (every core in this process's affinity mask), "
+                  f"os.cpu_count()={os.cpu_count()}, {cpu_model}",
         "us_per_layer": round(med * 1e6, 1),
     }
 
@@ -224,7 +249,7 @@ def main():
     gu_bytes = int(2 * wl.hidden * wl.intermediate * per + 2 * wl.tokens * wl.hidden)
     gu_ms = kern["gate_up"]
     gu_gbs = gu_bytes / (gu_ms / 1e3) / 1e9
-    traffic = read_traffic(wl.name)
+    traffic, traffic_src = read_traffic(wl.name)
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -247,8 +272,8 @@ def main():
         "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
         "roofline": {"kernel": "gate/up projection (gemv_kernel, 2 matrices)", "bound": "hbm",
                      "achieved": round(gu_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "algorithmic_bytes_per_launch": gu_bytes},
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                     "kernel_source_sha256": kernel_source_hash(), "algorithmic_bytes_per_launch": gu_bytes},
     }
     if wl.tokens > 32:  # many-token chunks run the matrix-core kernels: bound by the MFMA peak
         gu_flops = 4 * wl.tokens * wl.hidden * wl.intermediate

@@ -159,8 +159,15 @@ int qmlp_forward_rmsnorm(const void* h, const void* norm_w, float eps, const voi
                          const void* wd, void* out, void* ws, size_t ws_bytes, int M, int H, int I,
                          int fmt, int flags, qmlp_stream_t stream);
 
-/* Workspace bytes needed by qmlp_forward for these sizes (host only, no GPU needed). */
+/* Workspace bytes needed by qmlp_forward for these sizes (host only, no GPU needed).  The size
+ * never decreases as M grows, so a workspace sized for M serves every call with fewer tokens, and
+ * one workspace serves calls of different shapes as long as it is large enough for each. */
 size_t qmlp_workspace_bytes(int M, int H, int I, int fmt);
+
+/* The first QMLP_WS_COUNTER_BYTES bytes of every workspace hold arrival counters, at the same
+ * place for every shape.  They must read zero when a forward starts, and every forward leaves them
+ * zero.  The rest of the workspace may hold anything when a forward starts. */
+#define QMLP_WS_COUNTER_BYTES 524288
 
 /* Zero-fills the workspace with a kernel (not a memset node, so it may be graph-captured). */
 int qmlp_workspace_init(void* ws, size_t ws_bytes, qmlp_stream_t stream);

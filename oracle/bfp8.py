@@ -96,7 +96,26 @@ def quantize(w_bits, mantissa_bits=7):
 
 
 def dequantize(q, e8):
-    """Canonical bfp8 -> float32 ``q * 2**(e8 - 127)`` (exact; ``e8 == 0`` gives zeros)."""
+    """Canonical bfp8 -> float32 ``q * 2**(e8 - 127)`` (exact; ``e8 == 0`` gives zeros).
+
+    Computed in float32 when every product is a float32 number (|q| < 2**7 times a power of two
+    no larger than 2**121, i.e. ``e8 <= 248``, which covers every bf16 input), else in float64 and
+    rounded.  Both give the same bits wherever float32 can hold the exact value
+    (``dequantize_f64`` keeps the float64 form as the check)."""
+    q = np.asarray(q, dtype=np.int8)
+    e8 = np.asarray(e8, dtype=np.uint8)
+    if e8.size and int(e8.max()) > 248:
+        return dequantize_f64(q, e8)
+    rows, cols = q.shape
+    table = np.zeros(256, dtype=np.float32)
+    table[1:249] = np.ldexp(np.float32(1.0), np.arange(1, 249, dtype=np.int32) - 127)
+    out = q.astype(np.float32)
+    np.multiply(out.reshape(rows, cols // GROUP, GROUP), table[e8][..., None], out=out.reshape(rows, cols // GROUP, GROUP))
+    return out
+
+
+def dequantize_f64(q, e8):
+    """The float64 form of ``dequantize`` (rounded to float32 at the end)."""
     q = np.asarray(q, dtype=np.int8)
     e8 = np.asarray(e8, dtype=np.uint8)
     rows, cols = q.shape

@@ -34,15 +34,6 @@ def swiglu(x, wg, wu, wd, residual=None):
     return y.astype(np.float32)
 
 
-def swiglu_hidden(x, wg, wu):
-    """The intermediate ``silu(gate(x)) * up(x)`` in float32 (``fused_1d.py:10-22`` computes it on
-    device as the gate/up projection output)."""
-    x = np.asarray(x, dtype=np.float32)
-    g = x @ np.asarray(wg, dtype=np.float32).T
-    u = x @ np.asarray(wu, dtype=np.float32).T
-    return (silu(g) * u).astype(np.float32)
-
-
 def swiglu_torch(x, wg, wu, wd, residual=None):
     """The same formula with torch CPU tensors (float32), exactly the reference's expression
     ``(torch.nn.functional.silu(a @ G.T) * (a @ U.T)) @ D.T`` (``scripts/ci/mlp-sweep.py:126``)."""

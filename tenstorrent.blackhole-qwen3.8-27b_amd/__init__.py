@@ -11,6 +11,7 @@ from .mlp import (
     MLPWeights,
     PackedWeight,
     Qwen36MLP,
+    WorkspacePool,
     dequantize,
     load_mlp_weights,
     matrix_formats,
@@ -25,11 +26,12 @@ from .mlp import (
     unpack_bfp8,
     unpack_canonical,
     workspace_bytes,
+    workspace_pool,
 )
 
 __all__ = [
     "FMT_BF4", "FMT_BF16", "FMT_BFP8", "LIB_PATH", "QmlpError", "lib", "MATRIX_FORMATS", "WEIGHT_FORMATS",
     "MLPWeights", "PackedWeight", "Qwen36MLP", "dequantize", "load_mlp_weights", "matrix_formats", "mlp_forward",
     "mlp_forward_rmsnorm", "new_workspace", "pack_canonical", "pack_canonical_bfp8", "pack_weight", "quantize_bf4",
-    "quantize_bfp8", "unpack_bfp8", "unpack_canonical", "workspace_bytes",
+    "quantize_bfp8", "unpack_bfp8", "unpack_canonical", "workspace_bytes", "WorkspacePool", "workspace_pool",
 ]

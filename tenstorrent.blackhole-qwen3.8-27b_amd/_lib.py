@@ -17,6 +17,7 @@ FORMATS = {"bf16": FMT_BF16, "bfp8": FMT_BFP8, "bf4": FMT_BF4}
 QMLP_OK = 0
 OUT_F32 = 1
 RESIDUAL_F32 = 2
+WS_COUNTER_BYTES = 524288  # QMLP_WS_COUNTER_BYTES
 E_SHAPE, E_ALIGN, E_FORMAT, E_LAUNCH, E_WORKSPACE, E_NULL, E_DEVICE = -1, -2, -3, -4, -5, -6, -7
 _VALUE_ERRORS = {E_SHAPE, E_ALIGN, E_FORMAT, E_WORKSPACE, E_NULL}
 

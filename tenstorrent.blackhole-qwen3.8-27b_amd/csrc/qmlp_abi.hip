@@ -50,10 +50,15 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 WsLayout ws_layout(int M, int H, int I, int fmt) {
   WsLayout L{};
   size_t off = 0;
-  L.counters_gu = off;  // per tile (stream-K) or per tile group (split kernel): <= tiles
-  off = align256(off + (size_t)(I / kTileRows) * 4);
+  // Arrival counters, per tile (stream-K) or per tile group (split kernel): <= tiles.  They must
+  // read zero when a kernel starts and every kernel leaves them zero, so they sit at the same
+  // place for every shape, sized for the largest one: a workspace shared by calls of different
+  // shapes never has another call's data under a counter.
+  L.counters_gu = off;
+  off = align256(off + (size_t)(kMaxDim / kTileRows) * 4);
   L.counters_d = off;
-  off = align256(off + (size_t)(H / kTileRows) * 4);
+  off = align256(off + (size_t)(kMaxDim / kTileRows) * 4);
+  static_assert(2 * (kMaxDim / kTileRows) * 4 == QMLP_WS_COUNTER_BYTES, "counter region of the header");
   L.tx = off;
   off = align256(off + (size_t)M * 4);
   L.th = off;
@@ -63,11 +68,17 @@ WsLayout ws_layout(int M, int H, int I, int fmt) {
   L.h = off;
   off = align256(off + (size_t)M * I * 2);
   // partial-sum slots: the stream-K kernel (M <= 32) needs 2 per workgroup of NMAT x 2 token
-  // groups x 64 lanes x 16 B, the split kernel (M <= 32) one per (workgroup, tile) of NMAT x MG KB
+  // groups x 64 lanes x 16 B, the split kernel (M <= 32) one per (workgroup, tile) of NMAT x MG KB.
+  // Sized for every token count up to M (not just M itself), so that a workspace sized for M
+  // serves every smaller call: a 16-token call's split needs more slots than a 48-token call's
+  // tiled kernels, and the size must never shrink as M grows.
   const size_t sk_gu = (size_t)2 * kMaxWorkgroups * (2 * 2 * 64 * 16);
   const size_t sk_d = (size_t)2 * kMaxWorkgroups * (1 * 2 * 64 * 16);
-  const size_t gv_gu = M <= 32 ? gemv_part_bytes(I, H, 2, gemv_groups(M)) : 0;
-  const size_t gv_d = M <= 32 ? gemv_part_bytes(H, I, 1, gemv_groups(M)) : 0;
+  size_t gv_gu = 0, gv_d = 0;
+  for (int mg = 1; mg <= gemv_groups(std::min(M, 32)); ++mg) {
+    gv_gu = std::max(gv_gu, gemv_part_bytes(I, H, 2, mg));
+    gv_d = std::max(gv_d, gemv_part_bytes(H, I, 1, mg));
+  }
   L.part_gu = off;
   off = align256(off + std::max(sk_gu, gv_gu));
   L.part_d = off;
@@ -113,8 +124,8 @@ static int current_device_info(DeviceInfo* out) {
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 static bool shape_ok(int rows, int cols) {
-  return rows > 0 && cols > 0 && rows % kTileRows == 0 && cols % kSuperK == 0 && rows <= (1 << 20) &&
-         cols <= (1 << 20);
+  return rows > 0 && cols > 0 && rows % kTileRows == 0 && cols % kSuperK == 0 && rows <= kMaxDim &&
+         cols <= kMaxDim;
 }
 
 }  // namespace qmlp

@@ -37,6 +37,7 @@ int launch_dequant(const void* packed, int rows, int cols, int fmt, float* out, 
 int launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 
 constexpr int kMaxWorkgroups = 512;  // upper bound used to size the workspace
+constexpr int kMaxDim = 1 << 20;      // largest H, I, rows or cols the library accepts
 
 // 2-D split of one projection for the M <= 32 weight-streaming kernel (qmlp_gemv.hip).
 struct GemvPlan {

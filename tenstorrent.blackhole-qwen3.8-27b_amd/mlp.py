@@ -194,12 +194,64 @@ def workspace_bytes(M, H, I, fmt):
     return n
 
 
-def new_workspace(M, H, I, fmt, device, stream=None):
-    """Allocate and initialise a forward workspace (outside any graph capture)."""
-    n = workspace_bytes(M, H, I, fmt)
+def _new_workspace_bytes(n, device, stream=None):
     ws = torch.empty(n, dtype=torch.uint8, device=device)
     _lib.check(_lib.lib().qmlp_workspace_init(_lib.ptr(ws), n, _lib.stream_handle(stream)), "qmlp_workspace_init")
     return ws
+
+
+def new_workspace(M, H, I, fmt, device, stream=None):
+    """Allocate and initialise a forward workspace (outside any graph capture).  A workspace sized
+    for M tokens serves every call with M or fewer tokens, of any shape whose size fits."""
+    return _new_workspace_bytes(workspace_bytes(M, H, I, fmt), device, stream)
+
+
+class WorkspacePool:
+    """One forward workspace per (device, stream), shared by every MLP that runs there.
+
+    Forwards on one stream run one after another, so they can share a workspace.  Forwards on
+    different streams may overlap, so each stream gets its own.  A workspace only grows, and only
+    outside graph capture: during a capture the stream must already hold a large enough one.  Run
+    one forward on that stream first, or call ``reserve``.  The reference keeps one scratch buffer
+    per device for all layers in the same way (``docker/qwen-c2-graft/graft/mlp.py:274-356``).
+    """
+
+    def __init__(self):
+        self._ws = {}
+
+    @staticmethod
+    def _key(device, stream):
+        s = stream if stream is not None else torch.cuda.current_stream(device)
+        return (torch.device(device).index if torch.device(device).index is not None else torch.cuda.current_device(),
+                s.cuda_stream)
+
+    def reserve(self, nbytes, device, stream=None):
+        """The workspace of (device, stream), grown to at least ``nbytes`` (outside capture only)."""
+        key = self._key(device, stream)
+        ws = self._ws.get(key)
+        if ws is None or ws.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise ValueError(f"no workspace of {nbytes} bytes for stream {key[1]:#x} during graph capture: run one "
+                                 "forward on the capturing stream before capturing, or call WorkspacePool.reserve")
+            if ws is not None:
+                nbytes = max(nbytes, ws.numel())
+            # allocated with the stream current, so that the caching allocator hands the memory of a
+            # replaced workspace only to later work on this stream (stream-ordered after its last use)
+            s = stream if stream is not None else torch.cuda.current_stream(device)
+            with torch.cuda.stream(s):
+                ws = _new_workspace_bytes(nbytes, device, s)
+            self._ws[key] = ws
+        return ws
+
+    def total_bytes(self):
+        return sum(ws.numel() for ws in self._ws.values())
+
+    def clear(self):
+        self._ws.clear()
+
+
+# Shared by every Qwen36MLP unless one is given its own pool.
+workspace_pool = WorkspacePool()
 
 
 @dataclass(frozen=True)
@@ -228,13 +280,15 @@ class MLPWeights:
         return self.w1.stream_bytes + self.w2.stream_bytes + self.w3.stream_bytes
 
 
-def load_mlp_weights(device, state_dict, tensor_cache_path=None, args=None, weight_format="bfp8"):
+def load_mlp_weights(device, state_dict, tensor_cache_path=None, args=None, weight_format="bfp8", strict=True):
     """Per-layer MLP state -> MLPWeights (``mlp.py:45-169``).
 
     ``state_dict`` holds ``gate_proj.weight`` / ``up_proj.weight`` ``[I, H]`` and
     ``down_proj.weight`` ``[H, I]`` (HF layout).  ``tensor_cache_path`` (a directory) enables the
     on-disk cache of packed weights, like the reference's ``cache_file_name``.  ``weight_format``
-    may also come from ``args.mlp_weight_format``.
+    may also come from ``args.mlp_weight_format``.  A cache entry passes the same checks as a fresh
+    conversion: with ``strict`` it must hold no flushed groups, and its shape must match the
+    state-dict tensor when the state dict has one.
     """
     fmt = getattr(args, "mlp_weight_format", weight_format) if args is not None else weight_format
     gu_fmt, down_fmt = matrix_formats(fmt)
@@ -252,13 +306,26 @@ def load_mlp_weights(device, state_dict, tensor_cache_path=None, args=None, weig
             cache = weight_cache.cache_file(tensor_cache_path, name, mfmt)
             pw = weight_cache.load(cache, device) if os.path.exists(cache) else None
             if pw is not None:
+                if pw.fmt != mfmt:
+                    raise ValueError(f"cache entry {cache} holds {pw.fmt}, expected {mfmt}")
+                src = state_dict.get(f"{name}.weight") if hasattr(state_dict, "get") else None
+                if src is not None and tuple(src.shape) != (pw.rows, pw.cols):
+                    raise ValueError(f"cache entry {cache} is [{pw.rows}, {pw.cols}] but {name}.weight is "
+                                     f"{list(src.shape)}: stale cache")
+                header = (pw.max_row_norm, pw.flushed_groups)
+                _read_info(pw)  # the trailer the kernels read, not the file header's copy of it
+                if header != (pw.max_row_norm, pw.flushed_groups):
+                    raise ValueError(f"cache entry {cache}: header and packed trailer disagree")
+                if strict and pw.flushed_groups:
+                    raise ValueError(f"cache entry {cache}: {pw.flushed_groups} {mfmt} groups lie more than 19 "
+                                     "binades below their row maximum")
                 packed[field] = pw
                 continue
         w = state_dict[f"{name}.weight"]
         if not isinstance(w, torch.Tensor):
             w = torch.as_tensor(w)
         w = w.to(device=device, dtype=torch.bfloat16).contiguous()
-        packed[field] = pack_weight(w, mfmt)
+        packed[field] = pack_weight(w, mfmt, strict=strict)
         del w
         if cache is not None:
             from . import weight_cache
@@ -361,35 +428,36 @@ class Qwen36MLP:
     """SwiGLU feed-forward network (``docker/qwen-c2-graft/graft/mlp.py:359-423``) on MI355X.
 
     ``Qwen36MLP(device, state_dict, tensor_cache_path=None, args=None, tt_ccl=None,
-    weight_format="bfp8", max_tokens=2048)``; ``forward(x, residual=None, out=None)``.
-    The workspace for up to ``max_tokens`` rows is allocated here, so ``forward`` allocates
-    nothing but its output (and nothing at all when ``out`` is given): it may run inside a HIP
-    graph capture.
+    weight_format="bfp8", max_tokens=2048, pool=None)``; ``forward(x, residual=None, out=None)``.
+    Every instance takes its workspace from ``pool`` (the module's shared ``workspace_pool`` by
+    default): one workspace per (device, stream) for all layers, reserved here for up to
+    ``max_tokens`` rows on the current stream.  ``forward`` allocates nothing but its output (and
+    nothing at all when ``out`` is given), so it may run inside a HIP graph capture on a stream that
+    already holds a large enough workspace.
     """
 
     def __init__(self, mesh_device, state_dict, tensor_cache_path=None, args=None, tt_ccl=None,
-                 weight_format="bfp8", max_tokens=2048):
+                 weight_format="bfp8", max_tokens=2048, pool=None):
         self.device = torch.device(mesh_device) if not isinstance(mesh_device, torch.device) else mesh_device
         self.args = args
         self.tt_ccl = tt_ccl
         self.weights = load_mlp_weights(self.device, state_dict, tensor_cache_path, args, weight_format)
         self.max_tokens = int(max_tokens)
-        self._workspace = new_workspace(self.max_tokens, self.weights.hidden, self.weights.intermediate,
-                                        self.weights.fmt, self.device)
+        self.pool = workspace_pool if pool is None else pool
+        self.pool.reserve(self._workspace_bytes(self.max_tokens), self.device)
 
     @property
     def weight_format(self):
         return self.weights.fmt
 
+    def _workspace_bytes(self, M):
+        return workspace_bytes(M, self.weights.hidden, self.weights.intermediate, self.weights.fmt)
+
     def _workspace_for(self, M):
-        if M > self.max_tokens:
-            # Outside graph capture only: grow once.
-            if torch.cuda.is_current_stream_capturing():
-                raise ValueError(f"M={M} exceeds max_tokens={self.max_tokens} during graph capture")
+        # sizes never shrink as M grows, so the reservation for max_tokens covers every smaller call
+        if M > self.max_tokens and not torch.cuda.is_current_stream_capturing():
             self.max_tokens = M
-            self._workspace = new_workspace(M, self.weights.hidden, self.weights.intermediate, self.weights.fmt,
-                                            self.device)
-        return self._workspace
+        return self.pool.reserve(self._workspace_bytes(max(M, self.max_tokens)), self.device)
 
     def forward(self, x, residual=None, out=None, out_dtype=None):
         if not isinstance(x, torch.Tensor) or x.dtype != torch.bfloat16:

@@ -1,0 +1,79 @@
+"""Shared helpers of the GPU parity tests: identically dequantised host weights, the oracle call
+and the stated bar (max|out - oracle| <= 1e-2 * RMS(oracle); a bf16 output also gets half a bf16
+ulp of the oracle value)."""
+import numpy as np
+
+from oracle import bf16 as obf16
+from oracle import bfp8 as obfp8
+from oracle import mlp as omlp
+
+TOL = 1e-2
+
+
+def bits(t):
+    import torch
+
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def host_matrix(pkg, w, mfmt):
+    """fp32 host copy of one bf16 GPU matrix as the kernels see it in matrix format ``mfmt``."""
+    if mfmt in ("bfp8", "bf4"):
+        q, e8 = pkg.quantize_bf4(w) if mfmt == "bf4" else pkg.quantize_bfp8(w)
+        return obfp8.dequantize(q.cpu().numpy(), e8.cpu().numpy())
+    return obf16.bits_to_f32(bits(w))
+
+
+def host_weights(pkg, sd, fmt):
+    """fp32 host copies of the identically dequantised weights (keyed by HF name)."""
+    gu_fmt, down_fmt = pkg.matrix_formats(fmt)
+    return {name: host_matrix(pkg, sd[f"{name}.weight"], down_fmt if name == "down_proj" else gu_fmt)
+            for name in ("gate_proj", "up_proj", "down_proj")}
+
+
+def oracle(xf, hw, residual=True):
+    return omlp.swiglu(xf, hw["gate_proj"], hw["up_proj"], hw["down_proj"], residual=xf if residual else None)
+
+
+def check(y, ref, what):
+    """The stated bar on an fp32 (unrounded) output; returns err / bound."""
+    ok, err, bound = omlp.tolerance_ok(y, ref, TOL)
+    print(f"{what}: max|err|={err:.4e} bound={bound:.4e} ({err / bound:.2f} of the bar)", flush=True)
+    assert ok, f"{what}: {err} > {bound}"
+    return err / bound
+
+
+def check_bf16(y, ref, what):
+    """A bf16 output cannot be closer to the fp32 oracle than its own rounding: elementwise
+    |y - ref| <= 1e-2 * RMS(ref) + half a bf16 ulp of ref."""
+    ok, worst, bound = omlp.tolerance_ok_bf16(y, ref, TOL)
+    print(f"{what} (bf16 out): max(|err| - half ulp)={worst:.4e} bar={bound:.4e}", flush=True)
+    assert ok, f"{what}: {worst} > {bound}"
+
+
+def worst_row_ratio(y, ref):
+    """max over token rows of max|y - ref| / (1e-2 * RMS of that row of ref): the bar applied row
+    by row (a diagnostic for inputs whose rows differ by orders of magnitude)."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    rms = np.sqrt(np.mean(ref * ref, axis=1))
+    err = np.max(np.abs(y - ref), axis=1)
+    return float(np.max(err / (TOL * np.maximum(rms, 1e-300))))
+
+
+def check_rows(y, ref, what, bf16_out=False):
+    """The stated bar applied to each token row on its own (every row of the MLP is an
+    independent forward): max|y_m - ref_m| <= 1e-2 * RMS(ref_m) for every row m (plus half a bf16
+    ulp of ref for a bf16 output).  Returns the worst row's ratio."""
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    rms = np.sqrt(np.mean(ref * ref, axis=1))
+    dev = np.abs(y - ref)
+    if bf16_out:
+        _, e = np.frexp(np.abs(ref))
+        dev = dev - np.ldexp(1.0, e - 9)
+    ratio = np.max(dev, axis=1) / (TOL * np.maximum(rms, 1e-300))
+    worst = float(np.max(ratio))
+    print(f"{what}: worst row at {worst:.2f} of the per-row bar (row {int(np.argmax(ratio))})", flush=True)
+    assert worst <= 1.0, f"{what}: row {int(np.argmax(ratio))} at {worst:.3f} of the bar"
+    return worst

@@ -63,6 +63,20 @@ def test_workspace_bytes(pkg):
     assert lib.qmlp_workspace_bytes(16, 5120, 17408, 3) == 0
 
 
+@pytest.mark.parametrize("H,I", [(5120, 17408), (1024, 3072), (5120, 8704), (256, 76800)])
+@pytest.mark.parametrize("fmt", [0, 1, 2])
+def test_workspace_bytes_never_shrink_as_m_grows(pkg, H, I, fmt):
+    """A workspace sized for M tokens serves every call with fewer tokens: the size is
+    non-decreasing in M (the split kernels' partial slots at M <= 32 can exceed what 33..~400
+    tokens need otherwise)."""
+    lib = pkg.lib()
+    Ms = list(range(1, 65)) + [100, 200, 373, 374, 512, 1024, 2048]
+    sizes = [lib.qmlp_workspace_bytes(M, H, I, fmt) for M in Ms]
+    assert all(s > 0 for s in sizes)
+    for (m0, s0), (m1, s1) in zip(zip(Ms, sizes), zip(Ms[1:], sizes[1:])):
+        assert s1 >= s0, f"workspace shrinks from M={m0} ({s0} B) to M={m1} ({s1} B)"
+
+
 def test_forward_argument_errors_need_no_gpu(pkg):
     lib = pkg.lib()
     p = ctypes.c_void_p(1 << 20)          # never dereferenced: validation fails first

@@ -12,48 +12,8 @@ from oracle import mlp as omlp
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-2
-
-
-def _bits(t):
-    import torch
-
-    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-
-
-def _host_weights(pkg, sd, fmt):
-    """fp32 host copies of the identically dequantised weights (keyed by HF name)."""
-    out = {}
-    gu_fmt, down_fmt = pkg.matrix_formats(fmt)
-    for name in ("gate_proj", "up_proj", "down_proj"):
-        w = sd[f"{name}.weight"]
-        mfmt = down_fmt if name == "down_proj" else gu_fmt
-        if mfmt in ("bfp8", "bf4"):
-            q, e8 = pkg.quantize_bf4(w) if mfmt == "bf4" else pkg.quantize_bfp8(w)
-            out[name] = obfp8.dequantize(q.cpu().numpy(), e8.cpu().numpy())
-        else:
-            out[name] = obf16.bits_to_f32(_bits(w))
-    return out
-
-
-def _oracle(xf, hw, residual=True):
-    return omlp.swiglu(xf, hw["gate_proj"], hw["up_proj"], hw["down_proj"], residual=xf if residual else None)
-
-
-def _check(y, ref, what):
-    """The stated bar on an fp32 (unrounded) output."""
-    ok, err, bound = omlp.tolerance_ok(y, ref, TOL)
-    print(f"{what}: max|err|={err:.4e} bound={bound:.4e} ({err / bound:.2f} of the bar)", flush=True)
-    assert ok, f"{what}: {err} > {bound}"
-    return err / bound
-
-
-def _check_bf16(y, ref, what):
-    """A bf16 output cannot be closer to the fp32 oracle than its own rounding: elementwise
-    |y - ref| <= 1e-2 * RMS(ref) + half a bf16 ulp of ref."""
-    ok, worst, bound = omlp.tolerance_ok_bf16(y, ref, TOL)
-    print(f"{what} (bf16 out): max(|err| - half ulp)={worst:.4e} bar={bound:.4e}", flush=True)
-    assert ok, f"{what}: {worst} > {bound}"
+from parity_helpers import TOL, bits as _bits, check as _check, check_bf16 as _check_bf16  # noqa: E402
+from parity_helpers import host_weights as _host_weights, oracle as _oracle  # noqa: E402
 
 
 # ---------------------------------------------------------------- load-time kernels (bit-exact)
@@ -320,7 +280,7 @@ def test_graph_capture_replays(pkg, cuda, fmt):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):  # the warm-up gave this stream its workspace
         mlp.forward(static_x, residual=static_x, out=static_out)
     for seed in range(5):
         new_x = workloads.activations(M, H, seed=100 + seed, device=cuda)
@@ -514,7 +474,8 @@ def test_verify_arm_routes_decoder_mlps(pkg, cuda):
     with arm.install():
         out16, out8 = run(h16), run(h8)
     torch.cuda.synchronize()
-    assert arm.audit == dict(rows=16, layers=2, hits=[1, 1], fallbacks=[1, 1], restored=True)
+    assert arm.audit == dict(rows=16, layers=2, hits=[1, 1], fallbacks=[1, 1], restored=True,
+                          weights_unchanged=True)
     assert torch.equal(out8, ref8)  # fell back to the torch path
     # The torch decoder rounds the MLP output to bf16 before the residual add, the library rounds
     # the sum once: besides the 1e-2 * RMS bar allow two bf16 ulps of the reference per element.

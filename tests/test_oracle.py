@@ -113,6 +113,23 @@ def test_dequantised_groups_are_block_float_exact():
         assert np.abs(q.astype(np.int32)).max() <= 127
 
 
+def test_dequantise_float32_form_matches_float64_everywhere():
+    """Every (mantissa, exponent) pair: the float32 dequantiser equals the float64 form bit for bit,
+    and both equal the closed form q * 2^(e8 - 127) built with Python's exact ldexp."""
+    import math
+
+    qs = np.arange(-127, 128, dtype=np.int8)
+    for e8 in range(256):
+        q = np.tile(qs, 1)[None, :240]  # 240 = 15 groups of 16
+        e = np.full((1, 15), e8, dtype=np.uint8)
+        a, b = bfp8.dequantize(q, e), bfp8.dequantize_f64(q, e)
+        if e8 <= 248:
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), e8
+        exact = np.array([0.0 if e8 == 0 else math.ldexp(float(v), e8 - 127) for v in q[0]])
+        with np.errstate(over="ignore"):
+            assert np.array_equal(b[0], exact.astype(np.float32)), e8
+
+
 def test_round_trip_exact_on_representable_groups():
     rng = np.random.RandomState(5)
     groups = 4096
