@@ -172,6 +172,21 @@ size_t qmlp_workspace_bytes(int M, int H, int I, int fmt);
 /* Zero-fills the workspace with a kernel (not a memset node, so it may be graph-captured). */
 int qmlp_workspace_init(void* ws, size_t ws_bytes, qmlp_stream_t stream);
 
+/* qmlp_forward_ex without a workspace argument.  No counterpart in the reference: this entry point
+ * is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The workspace is a QMLP_SCRATCH_BYTES array of device
+ * memory inside the library, one per GPU, held until the process ends; the call allocates and
+ * frees nothing.  It serves every call whose qmlp_workspace_bytes(M, H, I, fmt) fits, e.g. M <= 32
+ * at H = 5120, I = 17408; larger calls fail with QMLP_E_WORKSPACE.  The first call on a device
+ * looks up the array's address and zeroes its arrival counters (a kernel on `stream`).  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (several streams or host
+ * threads) race and must be serialised by the caller.  Arguments, constraints and results as
+ * qmlp_forward_ex. */
+#define QMLP_SCRATCH_BYTES 33554432
+int qmlp_forward_noalloc(const void* x, const void* wg, const void* wu, const void* wd,
+                         const void* residual, void* out, int M, int H, int I, int fmt, int flags,
+                         qmlp_stream_t stream);
+
 /* ---------------------------------------------------------------- profiling (host only)
  *
  * Per-kernel timing of the forward pass, the counterpart of the reference's per-op signposts

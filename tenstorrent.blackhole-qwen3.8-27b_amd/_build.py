@@ -9,7 +9,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libqwen_mlp.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["qmlp_abi.hip", "qmlp_pack.hip", "qmlp_prep.hip", "qmlp_gemv.hip", "qmlp_stream.hip", "qmlp_tiled.hip"]
+SOURCES = ["qmlp_abi.hip", "qmlp_pack.hip", "qmlp_prep.hip", "qmlp_gemv.hip", "qmlp_stream.hip", "qmlp_tiled.hip",
+           "qmlp_noalloc.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

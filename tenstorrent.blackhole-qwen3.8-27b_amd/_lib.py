@@ -18,6 +18,7 @@ QMLP_OK = 0
 OUT_F32 = 1
 RESIDUAL_F32 = 2
 WS_COUNTER_BYTES = 524288  # QMLP_WS_COUNTER_BYTES
+SCRATCH_BYTES = 33554432  # QMLP_SCRATCH_BYTES
 E_SHAPE, E_ALIGN, E_FORMAT, E_LAUNCH, E_WORKSPACE, E_NULL, E_DEVICE = -1, -2, -3, -4, -5, -6, -7
 _VALUE_ERRORS = {E_SHAPE, E_ALIGN, E_FORMAT, E_WORKSPACE, E_NULL}
 
@@ -42,6 +43,7 @@ SIGNATURES = {
     "qmlp_set_profile_events": (_I, [_P, _I]),
     "qmlp_plan_split": (_I, [_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int)]),
     "qmlp_forward_rmsnorm": (_I, [_P, _P, ctypes.c_float, _P, _P, _P, _P, _P, _SZ, _I, _I, _I, _I, _I, _P]),
+    "qmlp_forward_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
 }
 
 _lib = None

@@ -123,9 +123,65 @@ static int current_device_info(DeviceInfo* out) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+static bool known_fmt(int fmt) { return fmt == QMLP_FMT_BF16 || fmt == QMLP_FMT_BFP8 || fmt == QMLP_FMT_BF4; }
+
 static bool shape_ok(int rows, int cols) {
   return rows > 0 && cols > 0 && rows % kTileRows == 0 && cols % kSuperK == 0 && rows <= kMaxDim &&
          cols <= kMaxDim;
+}
+
+// Shared validation and dispatch of the forward entry points.
+int forward_impl(const char* fn, const void* x, const void* wg, const void* wu, const void* wd, const void* residual,
+                 void* out, void* ws, size_t ws_bytes, int M, int H, int I, int fmt, int flags, const void* normw,
+                 float eps, hipStream_t stream) {
+  if (!x || !wg || !wu || !wd || !out || !ws) return set_error(QMLP_E_NULL, "%s: null pointer", fn);
+  if (!known_fmt(fmt)) return set_error(QMLP_E_FORMAT, "%s: unknown format %d", fn, fmt);
+  if (flags & ~(QMLP_OUT_F32 | QMLP_RESIDUAL_F32)) return set_error(QMLP_E_FORMAT, "%s: unknown flags 0x%x", fn, flags);
+  if (M < 1 || M > 65536) return set_error(QMLP_E_SHAPE, "%s: M=%d out of range [1, 65536]", fn, M);
+  if (!shape_ok(16, H) || !shape_ok(16, I))
+    return set_error(QMLP_E_SHAPE, "%s: H=%d and I=%d must be positive multiples of 256", fn, H, I);
+  // the kernels address one activation matrix ([M, H] or [M, I], up to fp32) with 32-bit offsets
+  if ((uint64_t)M * (uint64_t)std::max(H, I) * 4u >= (1ull << 32))
+    return set_error(QMLP_E_SHAPE, "%s: M * max(H, I) = %llu exceeds 2^30 elements", fn,
+                     (unsigned long long)M * (unsigned long long)std::max(H, I));
+  if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(ws) ||
+      (residual && !aligned16(residual)) || (normw && !aligned16(normw)))
+    return set_error(QMLP_E_ALIGN, "%s: every pointer must be 16-byte aligned", fn);
+  if (normw && !(eps >= 0.0f)) return set_error(QMLP_E_SHAPE, "%s: eps must be >= 0", fn);
+  const size_t xbytes = (size_t)M * H * 2, obytes = (size_t)M * H * ((flags & QMLP_OUT_F32) ? 4 : 2);
+  const uintptr_t xb = (uintptr_t)x, ob = (uintptr_t)out;
+  if (!(normw && x == out) && xb < ob + obytes && ob < xb + xbytes)
+    return set_error(QMLP_E_SHAPE, "%s: out must not overlap x", fn);
+  if (residual && residual != out) {
+    const size_t rbytes = (size_t)M * H * ((flags & QMLP_RESIDUAL_F32) ? 4 : 2);
+    const uintptr_t rb = (uintptr_t)residual;
+    if (rb < ob + obytes && ob < rb + rbytes)
+      return set_error(QMLP_E_SHAPE, "%s: out may equal residual but must not partially overlap it", fn);
+  }
+  if (residual == out && residual && ((flags & QMLP_OUT_F32) != 0) != ((flags & QMLP_RESIDUAL_F32) != 0))
+    return set_error(QMLP_E_SHAPE, "%s: an in-place residual needs the same dtype as out", fn);
+  const WsLayout L = ws_layout(M, H, I, fmt);
+  if (ws_bytes < L.total)
+    return set_error(QMLP_E_WORKSPACE, "%s: workspace holds %zu bytes, needs %zu", fn, ws_bytes, L.total);
+  DeviceInfo di;
+  if (int rc = current_device_info(&di)) return rc;
+  ForwardArgs a{x, (const uint8_t*)wg, (const uint8_t*)wu, (const uint8_t*)wd, residual, out, (uint8_t*)ws,
+                M, H, I, fmt, (flags & QMLP_OUT_F32) ? 1 : 0, (flags & QMLP_RESIDUAL_F32) ? 1 : 0, normw, eps};
+  // M <= 32: split-K weight streaming with LDS-staged activations (the RMSNorm fused into its
+  // staging and epilogue); where no such split fits (a K too long for the staged activations, or
+  // a device too small for the split's registers), M <= 32: stream-K
+  // weight streaming with activations read from L2; larger M: the LDS-tiled matrix-core GEMM.
+  // The last two take the RMSNorm as a separate pass.
+  if (gemv_supported(M, H, I, di.num_cus)) return launch_forward_gemv(a, di.num_cus, (hipStream_t)stream);
+  if (normw) {
+    uint8_t* xn = (uint8_t*)ws + L.xn;
+    if (int rc = launch_rmsnorm(x, normw, eps, M, H, xn, (hipStream_t)stream)) return rc;
+    a.x = xn;
+    a.normw = nullptr;
+  }
+  if (stream_supported(M, H, I, di.num_cus)) return launch_forward_stream(a, di.num_cus, (hipStream_t)stream);
+  if (tiled_supported(M, H, I)) return launch_forward_tiled(a, di.num_cus, (hipStream_t)stream);
+  return set_error(QMLP_E_SHAPE, "%s: no kernel for M=%d H=%d I=%d", fn, M, H, I);
 }
 
 }  // namespace qmlp
@@ -137,8 +193,6 @@ extern "C" {
 const char* qmlp_last_error(void) { return g_err; }
 
 const char* qmlp_version(void) { return "qwen_mlp 0.1 gfx950"; }
-
-static bool known_fmt(int fmt) { return fmt == QMLP_FMT_BF16 || fmt == QMLP_FMT_BFP8 || fmt == QMLP_FMT_BF4; }
 
 size_t qmlp_packed_bytes(int rows, int cols, int fmt) {
   if (!shape_ok(rows, cols) || !known_fmt(fmt)) return 0;
@@ -238,60 +292,6 @@ int qmlp_workspace_init(void* ws, size_t ws_bytes, qmlp_stream_t stream) {
   DeviceInfo di;
   if (int rc = current_device_info(&di)) return rc;
   return launch_fill_zero(ws, ws_bytes, (hipStream_t)stream);
-}
-
-// Shared validation and dispatch of the forward entry points.
-static int forward_impl(const char* fn, const void* x, const void* wg, const void* wu, const void* wd,
-                        const void* residual, void* out, void* ws, size_t ws_bytes, int M, int H, int I, int fmt,
-                        int flags, const void* normw, float eps, qmlp_stream_t stream) {
-  if (!x || !wg || !wu || !wd || !out || !ws) return set_error(QMLP_E_NULL, "%s: null pointer", fn);
-  if (!known_fmt(fmt)) return set_error(QMLP_E_FORMAT, "%s: unknown format %d", fn, fmt);
-  if (flags & ~(QMLP_OUT_F32 | QMLP_RESIDUAL_F32)) return set_error(QMLP_E_FORMAT, "%s: unknown flags 0x%x", fn, flags);
-  if (M < 1 || M > 65536) return set_error(QMLP_E_SHAPE, "%s: M=%d out of range [1, 65536]", fn, M);
-  if (!shape_ok(16, H) || !shape_ok(16, I))
-    return set_error(QMLP_E_SHAPE, "%s: H=%d and I=%d must be positive multiples of 256", fn, H, I);
-  // the kernels address one activation matrix ([M, H] or [M, I], up to fp32) with 32-bit offsets
-  if ((uint64_t)M * (uint64_t)std::max(H, I) * 4u >= (1ull << 32))
-    return set_error(QMLP_E_SHAPE, "%s: M * max(H, I) = %llu exceeds 2^30 elements", fn,
-                     (unsigned long long)M * (unsigned long long)std::max(H, I));
-  if (!aligned16(x) || !aligned16(wg) || !aligned16(wu) || !aligned16(wd) || !aligned16(out) || !aligned16(ws) ||
-      (residual && !aligned16(residual)) || (normw && !aligned16(normw)))
-    return set_error(QMLP_E_ALIGN, "%s: every pointer must be 16-byte aligned", fn);
-  if (normw && !(eps >= 0.0f)) return set_error(QMLP_E_SHAPE, "%s: eps must be >= 0", fn);
-  const size_t xbytes = (size_t)M * H * 2, obytes = (size_t)M * H * ((flags & QMLP_OUT_F32) ? 4 : 2);
-  const uintptr_t xb = (uintptr_t)x, ob = (uintptr_t)out;
-  if (!(normw && x == out) && xb < ob + obytes && ob < xb + xbytes)
-    return set_error(QMLP_E_SHAPE, "%s: out must not overlap x", fn);
-  if (residual && residual != out) {
-    const size_t rbytes = (size_t)M * H * ((flags & QMLP_RESIDUAL_F32) ? 4 : 2);
-    const uintptr_t rb = (uintptr_t)residual;
-    if (rb < ob + obytes && ob < rb + rbytes)
-      return set_error(QMLP_E_SHAPE, "%s: out may equal residual but must not partially overlap it", fn);
-  }
-  if (residual == out && residual && ((flags & QMLP_OUT_F32) != 0) != ((flags & QMLP_RESIDUAL_F32) != 0))
-    return set_error(QMLP_E_SHAPE, "%s: an in-place residual needs the same dtype as out", fn);
-  const WsLayout L = ws_layout(M, H, I, fmt);
-  if (ws_bytes < L.total)
-    return set_error(QMLP_E_WORKSPACE, "%s: workspace holds %zu bytes, needs %zu", fn, ws_bytes, L.total);
-  DeviceInfo di;
-  if (int rc = current_device_info(&di)) return rc;
-  ForwardArgs a{x, (const uint8_t*)wg, (const uint8_t*)wu, (const uint8_t*)wd, residual, out, (uint8_t*)ws,
-                M, H, I, fmt, (flags & QMLP_OUT_F32) ? 1 : 0, (flags & QMLP_RESIDUAL_F32) ? 1 : 0, normw, eps};
-  // M <= 32: split-K weight streaming with LDS-staged activations (the RMSNorm fused into its
-  // staging and epilogue); where no such split fits (a K too long for the staged activations, or
-  // a device too small for the split's registers), M <= 32: stream-K
-  // weight streaming with activations read from L2; larger M: the LDS-tiled matrix-core GEMM.
-  // The last two take the RMSNorm as a separate pass.
-  if (gemv_supported(M, H, I, di.num_cus)) return launch_forward_gemv(a, di.num_cus, (hipStream_t)stream);
-  if (normw) {
-    uint8_t* xn = (uint8_t*)ws + L.xn;
-    if (int rc = launch_rmsnorm(x, normw, eps, M, H, xn, (hipStream_t)stream)) return rc;
-    a.x = xn;
-    a.normw = nullptr;
-  }
-  if (stream_supported(M, H, I, di.num_cus)) return launch_forward_stream(a, di.num_cus, (hipStream_t)stream);
-  if (tiled_supported(M, H, I)) return launch_forward_tiled(a, di.num_cus, (hipStream_t)stream);
-  return set_error(QMLP_E_SHAPE, "%s: no kernel for M=%d H=%d I=%d", fn, M, H, I);
 }
 
 int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* wd, const void* residual, void* out,

@@ -98,4 +98,10 @@ int plan_stream(int rows, int K, int num_cus, int* P, int* maxseg);
 bool stream_supported(int M, int H, int I, int num_cus);
 int launch_forward_stream(const ForwardArgs& a, int num_cus, hipStream_t s);
 
+// Argument validation and dispatch shared by every forward entry point (qmlp_abi.hip).  `fn` names
+// the entry point in error messages; normw != null selects the RMSNorm prologue.
+int forward_impl(const char* fn, const void* x, const void* wg, const void* wu, const void* wd, const void* residual,
+                 void* out, void* ws, size_t ws_bytes, int M, int H, int I, int fmt, int flags, const void* normw,
+                 float eps, hipStream_t stream);
+
 }  // namespace qmlp
