@@ -151,10 +151,11 @@ int qmlp_forward_ex(const void* x, const void* wg, const void* wu, const void* w
  *   h       bf16 [M, H], the pre-norm hidden state (also the residual)
  *   norm_w  bf16 [H]
  *   out     bf16 [M, H] (fp32 with QMLP_OUT_F32); may equal h (in-place residual update)
- * Other arguments and constraints as qmlp_forward_ex (QMLP_RESIDUAL_F32 is not accepted).  M <= 32
- * fuses the norm into the gate/up kernel (the channel gain into the activation staging, the
- * per-token 1/rms into the epilogue); larger M (and the long-K fallback) run it as one extra pass
- * over h. */
+ * Other arguments and constraints as qmlp_forward_ex (QMLP_RESIDUAL_F32 is not accepted).  n is
+ * rounded to bf16, as the reference's separate norm writes it.  M <= 32 fuses the norm into the
+ * gate/up kernel's activation staging (each workgroup reduces the whole row's sum of squares in
+ * one fixed order, so every K range of a token sees the same 1/rms); larger M (and the long-K
+ * fallback) run it as one extra pass over h. */
 int qmlp_forward_rmsnorm(const void* h, const void* norm_w, float eps, const void* wg, const void* wu,
                          const void* wd, void* out, void* ws, size_t ws_bytes, int M, int H, int I,
                          int fmt, int flags, qmlp_stream_t stream);

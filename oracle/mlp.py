@@ -18,16 +18,31 @@ def silu(v):
     return v / (one + np.exp(-v))
 
 
-def swiglu(x, wg, wu, wd, residual=None):
+def epilogue_h_bf16(g, u):
+    """The gate/up epilogue with a bf16 intermediate: ``h = bf16(silu(g) * u)`` from float32 g and
+    u, rounded once to nearest-even and returned as float32.  The reference's fused gate/up hands
+    the down projection a bf16 h (``scripts/ci/fused_1d.py:10-22,121``); its promoted register
+    epilogue rounds the fp32 product once (``scripts/ci/mlp_register_epilogue.py:13-30``), the rule
+    the bf16-weight kernels follow."""
+    from . import bf16 as obf16
+
+    g = np.asarray(g, dtype=np.float32)
+    u = np.asarray(u, dtype=np.float32)
+    return obf16.round_f32(silu(g) * u)
+
+
+def swiglu(x, wg, wu, wd, residual=None, h_bf16=False):
     """``residual + down(silu(gate(x)) * up(x))`` in float32.
 
-    x: [M, H]; wg, wu: [I, H] (out, in); wd: [H, I]; residual: [M, H] or None.
+    x: [M, H]; wg, wu: [I, H] (out, in); wd: [H, I]; residual: [M, H] or None.  With ``h_bf16`` the
+    intermediate h is rounded to bf16 once (``epilogue_h_bf16``) before the down projection, as the
+    bf16-weight path and the reference's fused gate/up keep it.
     Follows ``scripts/ci/mlp-sweep.py:121-126`` and ``layer.py:357``.
     """
     x = np.asarray(x, dtype=np.float32)
     g = x @ np.asarray(wg, dtype=np.float32).T
     u = x @ np.asarray(wu, dtype=np.float32).T
-    h = silu(g) * u
+    h = epilogue_h_bf16(g, u) if h_bf16 else silu(g) * u
     y = h @ np.asarray(wd, dtype=np.float32).T
     if residual is not None:
         y = y + np.asarray(residual, dtype=np.float32)

@@ -60,8 +60,8 @@ struct GvParams {
   const void* residual;   // down: [M, N] bf16 or fp32, may alias out
   int out_f32, res_f32;
   float* part;            // [P][G][NMAT * MG * 64] f32x4 partial slots
-  float* pss;             // [P][kPssStride] per-workgroup token sums: [0,32) of the staged values'
-                          // squares (h bound), [32,64) of the raw x squares (RMSNorm)
+  float* pss;             // [P][kPssStride] per-workgroup token sums of the staged values' squares
+                          // (h bound)
   int* counters;          // [Ng] arrival counters (left at zero)
 };
 
@@ -121,11 +121,41 @@ __device__ __forceinline__ void stage_b_issue(const GvParams& p, int k0, int kq,
   }
 }
 
-// With the RMSNorm prologue the staged value is x * (1 + w) (the per-token 1/rms is a scale of
-// the whole product and is applied in the epilogue), rounded once to the B operand's type.
+// Whole-row sum of squares of token row m (RMSNorm prologue): the TPR threads of the row read it
+// in 16-byte chunks, kNormBatch loads in flight, and reduce in a fixed order, so every workgroup
+// -- whatever its K range -- computes the same value for the same row.
+constexpr int kNormBatch = 8;
+template <int TPR>
+__device__ __forceinline__ float row_sum_squares(const GvParams& p, int m, int tl) {
+  const int nfull = p.K / (TPR * 8);
+  const uint16_t* row = p.src + (size_t)min(m, p.M - 1) * p.K;
+  float sx = 0.f;
+  for (int j0 = 0; j0 < nfull; j0 += kNormBatch) {
+    u32x4 t[kNormBatch];
+#pragma unroll
+    for (int b = 0; b < kNormBatch; ++b) t[b] = *(const u32x4*)(row + (tl + min(j0 + b, nfull - 1) * TPR) * 8);
+#pragma unroll
+    for (int b = 0; b < kNormBatch; ++b)
+      if (j0 + b < nfull)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float lo = bf16_to_f32((uint16_t)(t[b][i] & 0xffffu)), hi = bf16_to_f32((uint16_t)(t[b][i] >> 16));
+          sx = fmaf(lo, lo, sx);
+          sx = fmaf(hi, hi, sx);
+        }
+  }
+#pragma unroll
+  for (int o = TPR / 2; o > 0; o >>= 1) sx += __shfl_xor(sx, o);
+  return sx;
+}
+
+// With the RMSNorm prologue the staged value is the normalised activation
+// n = bf16(x * rs * (1 + w)), rs = 1 / sqrt(mean(x^2) + eps) over the whole row -- the bf16 tensor
+// the decoder's separate norm hands to the MLP (docker/qwen-c2-graft/graft/layer.py:352-357) --
+// then converted like any activation.
 template <int NW, int MAXCH, bool NORM, int MG>
 __device__ __forceinline__ void stage_b_finish(const GvParams& p, int kq, const BStage<MAXCH, NORM>& bs,
-                                               uint8_t* ldsb, int* lds_t, float* lds_ss, float* lds_sx) {
+                                               uint8_t* ldsb, int* lds_t, float* lds_ss) {
   constexpr int TPR = NW * 64 / (16 * MG);
   const int m = threadIdx.x / TPR, tl = threadIdx.x % TPR;
   const int nch = kq * kSuperK / (TPR * 8);
@@ -168,7 +198,6 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, int kq, const 
     if (tl == 0) {
       lds_t[m] = t;
       lds_ss[m] = ss;
-      lds_sx[m] = 0.f;
     }
     const uint32_t dd = (uint32_t)(112 - t) << 7;
     const u16x2 d2 = __builtin_bit_cast(u16x2, dd | (dd << 16));
@@ -187,19 +216,20 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, int kq, const 
     }
     return;
   }
-  auto value = [&](int c, int i, int hi, float& xr) {
-    const uint32_t xw = hi ? bs.v[c][i] >> 16 : bs.v[c][i] & 0xffffu;
-    xr = bf16_to_f32((uint16_t)xw);
+  float rs = 1.0f;
+  if constexpr (NORM) rs = 1.0f / sqrtf(row_sum_squares<TPR>(p, m, tl) / (float)p.K + p.eps);
+  auto value = [&](int c, int i, int hi) {
+    const float xr = bf16_to_f32((uint16_t)(hi ? bs.v[c][i] >> 16 : bs.v[c][i] & 0xffffu));
     if constexpr (NORM) {
-      const uint32_t ww = hi ? bs.w[c][i] >> 16 : bs.w[c][i] & 0xffffu;
-      return __builtin_fmaf(xr, bf16_to_f32((uint16_t)ww), xr);
+      const float wv = bf16_to_f32((uint16_t)(hi ? bs.w[c][i] >> 16 : bs.w[c][i] & 0xffffu));
+      return bf16_to_f32(f32_to_bf16(xr * rs * (1.0f + wv)));
     }
     return xr;
   };
-  // bfp8: value -> fp16 * 2^t with max|value| * 2^t in [2^14, 2^15) over this K range (exact
-  // unless a value is 2^31 times smaller than the range maximum).  The range's sums of squares
-  // feed the h bound (values) and the RMSNorm (raw x).
-  float mx = 0.f, ss = 0.f, sx = 0.f;
+  // block float: value -> fp16 * 2^t with max|value| * 2^t in [2^14, 2^15) over this K range
+  // (exact unless a value is 2^31 times smaller than the range maximum).  The range's sum of
+  // squares feeds the h bound.
+  float mx = 0.f, ss = 0.f;
 #pragma unroll
   for (int c = 0; c < MAXCH; ++c) {
     if (c < nch) {
@@ -207,11 +237,9 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, int kq, const 
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int hi = 0; hi < 2; ++hi) {
-          float xr;
-          const float v = value(c, i, hi, xr);
+          const float v = value(c, i, hi);
           mx = fmaxf(mx, fabsf(v));
           ss = fmaf(v, v, ss);
-          if constexpr (NORM) sx = fmaf(xr, xr, sx);
         }
       }
     }
@@ -221,7 +249,6 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, int kq, const 
   for (int o = TPR / 2; o > 0; o >>= 1) {
     mx = fmaxf(mx, __shfl_xor(mx, o));
     ss += __shfl_xor(ss, o);
-    if constexpr (NORM) sx += __shfl_xor(sx, o);
   }
   int e2 = 0;
   if (mx > 0.f) frexpf(mx, &e2);
@@ -229,7 +256,6 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, int kq, const 
   if (tl == 0) {
     lds_t[m] = t;
     lds_ss[m] = ss;
-    lds_sx[m] = sx;
   }
 #pragma unroll
   for (int c = 0; c < MAXCH; ++c) {
@@ -237,8 +263,7 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, int kq, const 
       uint32_t o[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float xr;
-        const float a = value(c, i, 0, xr), b = value(c, i, 1, xr);
+        const float a = value(c, i, 0), b = value(c, i, 1);
         if (p.x_scale)
           o[i] = (uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(a, t)) |
                  ((uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(b, t)) << 16);
@@ -394,8 +419,7 @@ __device__ __forceinline__ void epi_load(const GvParams& p, int t, int lane, Epi
 
 template <int WF, int NMAT, int MG>
 __device__ __forceinline__ void gepilogue(const GvParams& p, int t, const f32x4 (&tot)[NMAT][MG],
-                                          const EpiIn<NMAT, MG>& e, int lane, const int (&th)[MG],
-                                          const float (&rs)[MG]) {
+                                          const EpiIn<NMAT, MG>& e, int lane, const int (&th)[MG]) {
   const int nb = t * kTileRows + (lane >> 4) * 4;
 #pragma unroll
   for (int mg = 0; mg < MG; ++mg) {
@@ -405,7 +429,7 @@ __device__ __forceinline__ void gepilogue(const GvParams& p, int t, const f32x4 
     if constexpr (NMAT == 2) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        float g = tot[0][mg][v] * rs[mg], u = tot[1][mg][v] * rs[mg];  // rs: the token's 1/rms (1 without the norm)
+        float g = tot[0][mg][v], u = tot[1][mg][v];
         if constexpr (WF) {
           g = __builtin_amdgcn_ldexpf(g, (int)e.rexp[0][v]);
           u = __builtin_amdgcn_ldexpf(u, (int)e.rexp[1][v]);
@@ -458,7 +482,6 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int s_t[ROWS];
   __shared__ float s_ss[ROWS];
-  __shared__ float s_sx[ROWS];
   __shared__ int s_last;
   __shared__ int s_seg[NW][2];  // first and last tile of each wave's unit range (empty: 1 > -1)
   const int lane = threadIdx.x & 63;
@@ -500,7 +523,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
   stage_b_issue<NW, MAXCH, NORM, MG>(p, c0 * kSuperK, kq, bs);
   gload(s0, p, blk_base, P0, lw, le);
   gload(s1, p, blk_base, P1, lw, le);  // repeats stage 0 when nst == 1
-  stage_b_finish<NW, MAXCH, NORM, MG>(p, kq, bs, ldsb, s_t, s_ss, s_sx);
+  stage_b_finish<NW, MAXCH, NORM, MG>(p, kq, bs, ldsb, s_t, s_ss);
   gload(s2, p, blk_base, P2, lw, le);
   __syncthreads();
 
@@ -591,7 +614,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
   for (int k = 0; k < kEpt; ++k) epi_load<WF, NMAT, MG>(p, g * p.G + min(wave + k * NW, Gw - 1), lane, ein[k]);
   double gn = 0.0, un = 0.0;
-  if (p.x_scale || NORM) {
+  if (p.x_scale) {
     gn = __longlong_as_double((long long)p.tg->max_row_norm_bits);
     un = __longlong_as_double((long long)p.tu->max_row_norm_bits);
   }
@@ -648,11 +671,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
       for (int mg = 0; mg < MG; ++mg) store_coherent(prs, dst + (mat * MG + mg) * 1024u, sum[mat][mg]);
   }
-  if ((p.x_scale || NORM) && threadIdx.x < 2 * ROWS) {
-    const int r = threadIdx.x < ROWS ? threadIdx.x : threadIdx.x - ROWS;
-    __hip_atomic_store(p.pss + (size_t)w * kPssStride + (threadIdx.x < ROWS ? r : 32 + r),
-                       threadIdx.x < ROWS ? s_ss[r] : s_sx[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (p.x_scale && threadIdx.x < ROWS)
+    __hip_atomic_store(p.pss + (size_t)w * kPssStride + threadIdx.x, s_ss[threadIdx.x], __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -668,16 +689,14 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
   // split j of token 16 mg + m) and the first QB partial slots of each of the wave's first kEpt
   // tiles (indices clamped, so every load is unconditional; the extra copies are not summed).
   // Then the S values of every sum are added in K order (deterministic).
-  float ssl[MG], sxl[MG];
+  float ssl[MG];
   auto load_token_sums = [&](int q0) {
     const float* ps = p.pss + (size_t)(g * p.S + min(q0 + (lane >> 4), p.S - 1)) * kPssStride;
 #pragma unroll
-    for (int mg = 0; mg < MG; ++mg) {
+    for (int mg = 0; mg < MG; ++mg)
       ssl[mg] = __hip_atomic_load(ps + mg * 16 + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sxl[mg] = NORM ? __hip_atomic_load(ps + 32 + mg * 16 + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-    }
   };
-  if (p.x_scale || NORM) load_token_sums(0);
+  if (p.x_scale) load_token_sums(0);
   auto slot_src = [&](int qq, int tl) {
     return (uint32_t)(((g * p.S + min(qq, p.S - 1)) * p.G + tl) * SLOT + lane) * 16u;
   };
@@ -695,33 +714,25 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
     }
   }
   int th[MG];
-  float rs[MG];
 #pragma unroll
-  for (int mg = 0; mg < MG; ++mg) {
-    th[mg] = 0;
-    rs[mg] = 1.0f;
-  }
-  if (p.x_scale || NORM) {
-    float ss[MG], sx[MG];
+  for (int mg = 0; mg < MG; ++mg) th[mg] = 0;
+  if (p.x_scale) {
+    float ss[MG];
 #pragma unroll
-    for (int mg = 0; mg < MG; ++mg) ss[mg] = sx[mg] = 0.f;
+    for (int mg = 0; mg < MG; ++mg) ss[mg] = 0.f;
     for (int q0 = 0; q0 < p.S; q0 += 4) {
       if (q0 > 0) load_token_sums(q0);  // more than 4 splits: the next 4 token sums
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int mg = 0; mg < MG; ++mg) {
-          const float a = __shfl(ssl[mg], 16 * j + m), b = __shfl(sxl[mg], 16 * j + m);
-          if (q0 + j < p.S) {
-            ss[mg] += a;
-            sx[mg] += b;
-          }
+          const float a = __shfl(ssl[mg], 16 * j + m);
+          if (q0 + j < p.S) ss[mg] += a;
         }
     }
 #pragma unroll
     for (int mg = 0; mg < MG; ++mg) {
-      if constexpr (NORM) rs[mg] = 1.0f / sqrtf(sx[mg] / (float)p.K + p.eps);
-      const double bound = (double)ss[mg] * ((double)rs[mg] * rs[mg]) * gn * un * (1.0 + 1.0 / 64.0);
+      const double bound = (double)ss[mg] * gn * un * (1.0 + 1.0 / 64.0);
       int eb = 0;
       if (bound > 0.0) frexp(bound, &eb);
       th[mg] = bound > 0.0 ? 15 - eb : 0;
@@ -766,7 +777,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
           for (int mg = 0; mg < MG; ++mg) tot[mat][mg] += v[k][qq][mat][mg];
     sum_rest(tl, QB, tot);
-    gepilogue<WF, NMAT, MG>(p, g * p.G + tl, tot, ein[k], lane, th, rs);
+    gepilogue<WF, NMAT, MG>(p, g * p.G + tl, tot, ein[k], lane, th);
   }
   // tiles beyond kEpt per wave (groups of more than kEpt * NW tiles)
   for (int tl = wave + kEpt * NW; tl < Gw; tl += NW) {
@@ -778,7 +789,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
       for (int mg = 0; mg < MG; ++mg) tot[mat][mg] = f32x4{0.f, 0.f, 0.f, 0.f};
     sum_rest(tl, 0, tot);
-    gepilogue<WF, NMAT, MG>(p, g * p.G + tl, tot, e, lane, th, rs);
+    gepilogue<WF, NMAT, MG>(p, g * p.G + tl, tot, e, lane, th);
   }
 }
 

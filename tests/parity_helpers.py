@@ -31,8 +31,9 @@ def host_weights(pkg, sd, fmt):
             for name in ("gate_proj", "up_proj", "down_proj")}
 
 
-def oracle(xf, hw, residual=True):
-    return omlp.swiglu(xf, hw["gate_proj"], hw["up_proj"], hw["down_proj"], residual=xf if residual else None)
+def oracle(xf, hw, residual=True, h_bf16=False):
+    return omlp.swiglu(xf, hw["gate_proj"], hw["up_proj"], hw["down_proj"], residual=xf if residual else None,
+                       h_bf16=h_bf16)
 
 
 def check(y, ref, what):

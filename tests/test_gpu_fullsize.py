@@ -156,6 +156,12 @@ def heavy_state_dict(H, I, seed, device):
 # carries: fp16 rounds to 2^-12, and the reference's bf16 h to 2^-9.  So that case applies the bar
 # to each token row on its own: each row is an independent forward, and its bar is its own output
 # RMS.  This is stricter than the global bar for every row except the few largest.
+#
+# The bf16-weight path keeps the reference's bf16 intermediate (one rounding of silu(g) * u, the
+# reference's fused gate/up epilogue).  On outlier activations that rounding alone moves the output
+# by up to ~3x the bar from the all-fp32 formula, in the reference as here, so for that format the
+# oracle rounds h the same way (swiglu(..., h_bf16=True)); the block-float formats keep h in fp16
+# with a per-token scale and are held to the all-fp32 formula.
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
@@ -163,8 +169,6 @@ def test_heavy_tailed_every_width(pkg, cuda, fmt):
     """H = 1024, I = 3072 at M = 1, 16, 32 and 2048 (every row checked), fp32 and bf16 outputs."""
     import torch
 
-    if fmt == "bf16":
-        pytest.skip("pending: the bf16-weight path rounds h to bf16 (2^-9), 3x the bar on outlier activations")
     H, I = 1024, 3072
     sd = heavy_state_dict(H, I, 9100, cuda)
     w = pkg.load_mlp_weights(cuda, sd, weight_format=fmt)  # strict: no group left the window
@@ -181,7 +185,8 @@ def test_heavy_tailed_every_width(pkg, cuda, fmt):
             torch.cuda.synchronize()
             assert torch.equal(y32.to(torch.bfloat16), y16)
             xf = x.float().cpu().numpy()
-            ref, nref = oracle(xf, hw), oracle(xf, hw, residual=False)
+            hb = fmt == "bf16"
+            ref, nref = oracle(xf, hw, h_bf16=hb), oracle(xf, hw, residual=False, h_bf16=hb)
             if row_span:
                 check_rows(y32.cpu().numpy(), ref, what)
                 check_rows(y16.float().cpu().numpy(), ref, what + " (bf16 out)", bf16_out=True)
@@ -197,8 +202,6 @@ def test_heavy_tailed_27b(pkg, cuda, fmt):
     """The 27B shape at the verify widths and, on sampled rows, the prefill chunk."""
     import torch
 
-    if fmt == "bf16":
-        pytest.skip("pending: the bf16-weight path rounds h to bf16 (2^-9), 3x the bar on outlier activations")
     sd = heavy_state_dict(H27, I27, 9300, cuda)
     w = pkg.load_mlp_weights(cuda, sd, weight_format=fmt)
     hw = host_weights(pkg, sd, fmt)
@@ -211,7 +214,7 @@ def test_heavy_tailed_27b(pkg, cuda, fmt):
             y32 = pkg.mlp_forward(x, w, workspace=ws, out_dtype=torch.float32)
             torch.cuda.synchronize()
             rows = _sample_rows(M) if M > 64 else np.arange(M)
-            ref = oracle(x.float().cpu().numpy()[rows], hw, residual=False)
+            ref = oracle(x.float().cpu().numpy()[rows], hw, residual=False, h_bf16=fmt == "bf16")
             y = y32.cpu().numpy()[rows]
             if row_span:
                 check_rows(y, ref, what)
@@ -223,8 +226,6 @@ def test_heavy_tailed_rmsnorm_prologue(pkg, cuda):
     """The fused RMSNorm prologue (M <= 32) and its separate pass (M > 32) on heavy-tailed h: the
     norm equalises the rows, so the global bar applies."""
     import torch
-
-    pytest.skip("pending: the fused prologue does not round the normalised rows to bf16 as the reference does")
 
     H, I = 1024, 3072
     sd = heavy_state_dict(H, I, 9500, cuda)

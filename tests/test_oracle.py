@@ -55,6 +55,28 @@ def test_double_rounding_known_answer():
     s = omlp.silu(g)
     assert int(bf16.f32_to_bits(s * u)[0]) == 0xBEBF
     assert int(bf16.f32_to_bits(bf16.round_f32(s) * bf16.round_f32(u))[0]) == 0xBEC0
+    # the oracle's bf16 epilogue is the single rounding
+    assert int(bf16.f32_to_bits(omlp.epilogue_h_bf16(g, u))[0]) == 0xBEBF
+
+
+def test_swiglu_with_bf16_h_rounds_only_the_intermediate():
+    # With every weight and activation a small power of two the products and sums are exact, so
+    # the bf16 intermediate changes the result only through the rounding of h; an h that is
+    # already a bf16 value is left alone, one that is not moves to its nearest-even neighbour.
+    x = np.array([[0.5, 0.25]], dtype=np.float32)
+    wg = np.array([[2.0, 0.0], [0.0, 0.0]], dtype=np.float32)  # g = [1, 0]
+    wu = np.array([[1.0, 0.0], [0.0, 4.0]], dtype=np.float32)  # u = [0.5, 1]
+    wd = np.array([[1.0, 1.0]], dtype=np.float32)
+    h = omlp.silu(np.float32(1.0)) * np.float32(0.5)  # 0.36552..., not a bf16 value
+    exact = omlp.swiglu(x, wg, wu, wd)
+    rounded = omlp.swiglu(x, wg, wu, wd, h_bf16=True)
+    assert exact[0, 0] == np.float32(h)
+    assert rounded[0, 0] == bf16.round_f32(np.float32(h))[()]
+    assert rounded[0, 0] != exact[0, 0]
+    assert abs(float(rounded[0, 0]) - float(h)) <= 2.0 ** -9 * abs(float(h))
+    # h already on the bf16 grid (g = 0 gives h = 0): unchanged
+    x0 = np.zeros((1, 2), dtype=np.float32)
+    assert np.array_equal(omlp.swiglu(x0, wg, wu, wd, h_bf16=True), omlp.swiglu(x0, wg, wu, wd))
 
 
 def test_double_rounding_changes_a_large_share():
