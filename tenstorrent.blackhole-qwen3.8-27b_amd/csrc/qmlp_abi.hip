@@ -63,8 +63,6 @@ WsLayout ws_layout(int M, int H, int I, int fmt) {
   off = align256(off + (size_t)M * 4);
   L.th = off;
   off = align256(off + (size_t)M * 4);
-  L.x16 = off;
-  off = align256(off + (fmt != QMLP_FMT_BF16 ? (size_t)M * H * 2 : 0));
   L.h = off;
   off = align256(off + (size_t)M * I * 2);
   // partial-sum slots: the stream-K kernel (M <= 32) needs 2 per workgroup of NMAT x 2 token
@@ -85,6 +83,10 @@ WsLayout ws_layout(int M, int H, int I, int fmt) {
   off = align256(off + std::max(sk_d, gv_d));
   L.pss = off;
   off = align256(off + (size_t)kMaxWorkgroups * 64 * 4);
+  // x16 and xn are read only by the gate/up projection; the many-token down projection reuses
+  // both (adjacent) for the partial tiles of its K-split tail.
+  L.x16 = off;
+  off = align256(off + (fmt != QMLP_FMT_BF16 ? (size_t)M * H * 2 : 0));
   L.xn = off;  // bf16 [M, H]: the normalised activations when the RMSNorm runs as its own pass
   off = align256(off + (size_t)M * H * 2);
   L.total = off;

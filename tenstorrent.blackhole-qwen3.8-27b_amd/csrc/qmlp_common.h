@@ -83,6 +83,24 @@ __device__ __forceinline__ T ld_stream(const T* p) {  // streamed once: do not k
 // s_waitcnt operand: vector memory counter 0, export and LDS/scalar counters not waited on.
 constexpr int kWaitVmcnt0 = 0x0f70;
 
+// Partial sums cross workgroups (and XCDs) through device-coherent 16-byte buffer stores and loads
+// (the sc1 cache policy of agent-scope atomic accesses, on whole 16-byte lanes so that one
+// instruction writes or reads whole lines): coherent at the device level by themselves, so
+// publishing needs no L2 write-back and reading no L2 invalidation -- only the wait for the stores
+// before the arrival counter moves.  The descriptor's extent bounds every access.
+constexpr int kCoherent = 16;                 // buffer cache-policy operand: sc1
+constexpr int kBufferRsrcWord3 = 0x00020000;  // raw (untyped) buffer descriptor, gfx9
+__device__ __forceinline__ void store_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kCoherent);
+}
+__device__ __forceinline__ f32x4 load_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherent));
+}
+// Waits until this thread's global loads and stores have completed.  A workgroup barrier does not
+// wait for global stores, so every thread calls this before the barrier that precedes an arrival
+// counter: the counter then moves only after the stores it announces are visible device-wide.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); }
+
 // ---------------------------------------------------------------- bfp8 in-register dequant
 //
 // Mantissa byte u (excess-128) and the byte-permute constant 0x64 form the half 0x64uu = 1024+u.

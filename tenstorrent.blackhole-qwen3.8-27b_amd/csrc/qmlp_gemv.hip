@@ -275,26 +275,9 @@ __device__ __forceinline__ void stage_b_finish(const GvParams& p, int kq, const 
   }
 }
 
-// Partial sums cross workgroups (and XCDs) through device-coherent 16-byte buffer stores and loads
-// (the sc1 cache policy of agent-scope atomic accesses, on whole 16-byte lanes so that one
-// instruction writes or reads whole lines): coherent at the device level by themselves, so
-// publishing needs no L2 write-back and reading no L2 invalidation -- only the wait for the stores
-// before the arrival counter moves.  The descriptor's extent bounds every access.
-constexpr int kCoherent = 16;                   // buffer cache-policy operand: sc1
-constexpr int kBufferRsrcWord3 = 0x00020000;    // raw (untyped) buffer descriptor, gfx9
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const GvParams& p, int slot_f32x4) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)p.part, 0, p.P * p.G * slot_f32x4 * 16, kBufferRsrcWord3);
 }
-__device__ __forceinline__ void store_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kCoherent);
-}
-__device__ __forceinline__ f32x4 load_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherent));
-}
-// Waits until this thread's global loads and stores have completed.  A workgroup barrier does not
-// wait for global stores, so every thread calls this before the barrier that precedes an arrival
-// counter: the counter then moves only after the stores it announces are visible device-wide.
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); }
 
 // ---------------------------------------------------------------- main loop pieces
 

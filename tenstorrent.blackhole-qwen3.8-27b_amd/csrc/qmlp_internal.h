@@ -20,13 +20,21 @@ bool profile_events(int slot, hipEvent_t* start, hipEvent_t* stop);
 // Launches a hot-path kernel.  While timing is on, the launch goes through hipExtLaunchKernel so
 // that the dispatch's own start and end timestamps land in the slot's events (no marker packets
 // between the kernels, so the timed kernels run exactly as they do untimed).
+// A projection launched in several parts records the start event with its first part and the stop
+// event with its last (marks: bit 0 start, bit 1 stop).
 template <typename... Args>
-void launch_timed(int slot, void (*kern)(Args...), dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+void launch_timed_part(int slot, int marks, void (*kern)(Args...), dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                       Args... args) {
   hipEvent_t start, stop;
   if (profile_events(slot, &start, &stop))
-    hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)lds, s, start, stop, 0u, args...);
+    hipExtLaunchKernelGGL(kern, grid, block, (uint32_t)lds, s, (marks & 1) ? start : nullptr,
+                          (marks & 2) ? stop : nullptr, 0u, args...);
   else
     hipLaunchKernelGGL(kern, grid, block, lds, s, args...);
+}
+template <typename... Args>
+void launch_timed(int slot, void (*kern)(Args...), dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+  launch_timed_part(slot, 3, kern, grid, block, lds, s, args...);
 }
 
 // Load-time kernels (qmlp_pack.hip).

@@ -22,6 +22,9 @@
 // Epilogue (fp32 accumulators in registers): gate/up -> h = silu(g) * u rounded once (fp16 *
 // 2^th for bfp8, bf16 for bf16 weights); down -> out = residual + y.  No cross-workgroup
 // reduction: every output element is owned by one lane of one wave.
+#include <map>
+#include <mutex>
+
 #include "qmlp_common.h"
 #include "qmlp_internal.h"
 
@@ -35,6 +38,11 @@ struct TlParams {
   const uint16_t* src;   // [M, K] B rows: fp16 * 2^tsrc[m] (bfp8 weights) or bf16
   int M, K, N, C;        // N output features, C = K / 256
   int nbm;               // token blocks
+  int bn0;               // first feature block of this launch
+  int ks;                // down projection: K splits per tile (1: every block covers all of K)
+  float* part;           // ks > 1: fp32 partial tiles, [tile][K split][block's outputs]
+  int part_bytes;
+  int* counters;         // ks > 1: arrival counter per tile (left at zero)
   const int* tsrc;       // bfp8: per-token exponent of src
   const int* tout;       // bfp8 gate/up: h16 = h * 2^tout[m]
   void* out;             // gate/up: h [M, N] 16-bit; down: out [M, N] bf16 or fp32
@@ -52,39 +60,48 @@ template <int WF, int NMAT, int TPW, int MG, int NWV, int NBB>
 __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   constexpr int NT = NWV * 64;
   constexpr int SLOT = MG * 2048;      // LDS bytes of one 64-K step of B
-  constexpr int CPT = MG * 128 / NT;   // 16-byte B chunks per thread per step
-  static_assert(CPT * NT == MG * 128, "B chunks must divide evenly over the threads");
+  // 16-byte B chunks per loading thread per step; with fewer chunks than threads (one group of
+  // tokens) only the first NLD threads (whole waves) load
+  constexpr int CPT = (MG * 128 + NT - 1) / NT, NLD = MG * 128 / CPT;
+  static_assert(CPT * NLD == MG * 128 && NLD <= NT && NLD % 64 == 0, "B chunks must divide evenly over whole waves");
   constexpr int BLK = WF == 2 ? kBf4Block : (WF ? kBfp8Block : kBf16Block);
   constexpr int SB = WF ? 1024 : 2048;  // bytes of one bf16/bfp8 K-step inside a weight block
   extern __shared__ __align__(16) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int L = xcd_logical(blockIdx.x, gridDim.x);  // blocks sharing weights share an XCD
-  const int bn = L / p.nbm, bm = L % p.nbm;
+  // tile = (feature block, token block); with K splits, the ks blocks of a tile are consecutive
+  const int tile = L / p.ks, q = L % p.ks;
+  const int bn = p.bn0 + tile / p.nbm, bm = tile % p.nbm;
   const int m0 = bm * MG * 16;
   const int tile0 = (bn * NWV + wave) * TPW;
-  const int nst = p.C * kSteps;
+  // K range of this block: superblocks [q C / ks, (q + 1) C / ks), steps counted from kbase
+  const int kbase = q * p.C / p.ks * kSteps;
+  const int nst = (q + 1) * p.C / p.ks * kSteps - kbase;
 
   // B chunk c = threadIdx.x + i * NT: token row r = c / 8, 8 K values j = c % 8 of the step;
   // quarter j / 2, half j % 2.  Rows beyond M repeat row M - 1 (their outputs are not stored).
   uint32_t goff[CPT], loff[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int c = threadIdx.x + i * NT, r = c >> 3, j = c & 7;
+    const int c = min((int)threadIdx.x, NLD - 1) + i * NLD, r = c >> 3, j = c & 7;
     const int mr = min(m0 + r, p.M - 1);
     goff[i] = (uint32_t)(mr * p.K + j * 8) * 2u;
     loff[i] = (uint32_t)(r >> 4) * 2048u + bfrag_off(j >> 1, r & 15, j & 1);
   }
   const uint8_t* srcb = (const uint8_t*)p.src;
+  const bool loader = NLD == NT || (int)threadIdx.x < NLD;  // whole waves
   auto bload = [&](u32x4(&v)[CPT], int step) {
-    const uint8_t* base = srcb + (size_t)min(step, nst - 1) * 128;
+    const uint8_t* base = srcb + (size_t)(kbase + min(step, nst - 1)) * 128;
+    if (loader)
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) v[i] = *(const u32x4*)(base + goff[i]);
+      for (int i = 0; i < CPT; ++i) v[i] = *(const u32x4*)(base + goff[i]);
   };
   auto bstore = [&](const u32x4(&v)[CPT], int step) {
     uint8_t* slot = lds + (step % 3) * SLOT;
+    if (loader)
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) *(u32x4*)(slot + loff[i]) = v[i];
+      for (int i = 0; i < CPT; ++i) *(u32x4*)(slot + loff[i]) = v[i];
   };
 
   const uint8_t* wt[NMAT][TPW];
@@ -96,7 +113,7 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   // Weights are re-read by every token block of the same features, so they are loaded with the
   // default cache policy (kept in L2 for the neighbouring blocks of the XCD).
   auto wload = [&](TlStage<WF, NMAT, TPW>& st, int step) {
-    const int sc = min(step, nst - 1);
+    const int sc = kbase + min(step, nst - 1);  // kbase is a multiple of 4: sc & 3 == step & 3
     const uint32_t off = (uint32_t)(sc >> 2) * BLK +
                          (WF == 2 ? (uint32_t)(sc & 2) * 512u + (uint32_t)(sc & 1) * 8u : (uint32_t)(sc & 3) * SB);
 #pragma unroll
@@ -229,6 +246,39 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
     if (r > 4) iter(s1, b1, b2, s + 4);
   }
 
+  if constexpr (NMAT == 1) {
+    if (p.ks > 1) {
+      // K-split tail: publish the partial tile, arrive; the last of the tile's ks blocks adds
+      // the ks partials in K order (deterministic) and runs the epilogue.
+      __shared__ int s_last;
+      const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(p.part, 0, p.part_bytes, kBufferRsrcWord3);
+      auto slot = [&](int qq, int t, int g) {  // byte offset of this lane's f32x4 in split qq's tile
+        return (uint32_t)(((((size_t)tile * p.ks + qq) * NWV + wave) * TPW * MG + t * MG + g) * 64 + lane) * 16u;
+      };
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int g = 0; g < MG; ++g) store_coherent(prs, slot(q, t, g), acc[0][t][g]);
+      wait_stores();
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(p.counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == p.ks - 1;
+        if (s_last) __hip_atomic_store(p.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (!s_last) return;
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int g = 0; g < MG; ++g) {
+          f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int qq = 0; qq < p.ks; ++qq) sum += qq == q ? acc[0][t][g] : load_coherent(prs, slot(qq, t, g));
+          acc[0][t][g] = sum;
+        }
+    }
+  }
+
   // epilogue: lane l holds features 4 * (l / 16) + v of each tile for token l % 16 of each group
   const int col = lane & 15, rq = (lane >> 4) * 4;
 #pragma unroll
@@ -321,14 +371,15 @@ template <int WF, int MG, int NBB>
 __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   constexpr int NWV = 8, NT = NWV * 64;
   constexpr int SLOT = MG * 4096;     // LDS bytes of one 64-K step of B
-  constexpr int CPT = MG * 256 / NT;  // 16-byte B chunks per thread per step
-  static_assert(CPT * NT == MG * 256, "B chunks must divide evenly over the threads");
+  // 16-byte B chunks per loading thread per step (one group of tokens: the first NLD threads)
+  constexpr int CPT = (MG * 256 + NT - 1) / NT, NLD = MG * 256 / CPT;
+  static_assert(CPT * NLD == MG * 256 && NLD <= NT && NLD % 64 == 0, "B chunks must divide evenly over whole waves");
   constexpr int BLK = WF == 2 ? kBf4Block : (WF ? kBfp8Block : kBf16Block);
   extern __shared__ __align__(16) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int L = xcd_logical(blockIdx.x, gridDim.x);  // blocks sharing weights share an XCD
-  const int bn = L / p.nbm, bm = L % p.nbm;
+  const int bn = p.bn0 + L / p.nbm, bm = L % p.nbm;
   const int m0 = bm * MG * 32;
   const int pair = bn * NWV + wave;
   const int nst = p.C * kSteps;
@@ -338,21 +389,24 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   uint32_t goff[CPT], loff[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
-    const int c = threadIdx.x + i * NT, r = c >> 3, k8 = c & 7;
+    const int c = min((int)threadIdx.x, NLD - 1) + i * NLD, r = c >> 3, k8 = c & 7;
     const int mr = min(m0 + r, p.M - 1);
     goff[i] = (uint32_t)(mr * p.K + k8 * 8) * 2u;
     loff[i] = (uint32_t)(r >> 5) * 4096u + b32_slot(k8 & 3, 32 * (k8 >> 2) + (r & 31)) * 16u;
   }
   const uint8_t* srcb = (const uint8_t*)p.src;
+  const bool loader = NLD == NT || (int)threadIdx.x < NLD;  // whole waves
   auto bload = [&](u32x4(&v)[CPT], int step) {
     const uint8_t* base = srcb + (size_t)min(step, nst - 1) * 128;
+    if (loader)
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) v[i] = *(const u32x4*)(base + goff[i]);
+      for (int i = 0; i < CPT; ++i) v[i] = *(const u32x4*)(base + goff[i]);
   };
   auto bstore = [&](const u32x4(&v)[CPT], int step) {
     uint8_t* slot = lds + (step % 3) * SLOT;
+    if (loader)
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) *(u32x4*)(slot + loff[i]) = v[i];
+      for (int i = 0; i < CPT; ++i) *(u32x4*)(slot + loff[i]) = v[i];
   };
 
   const int hk = lane >> 5;
@@ -542,14 +596,74 @@ constexpr int kTlNWV = 8;  // waves per block
 constexpr int kTlGuTPW = 1, kTlGuMG = 8;
 constexpr int kTlDnTPW = 2, kTlDnMG = 4;
 
+// Resident blocks per CU of a kernel (its registers and LDS), once per kernel; 1 if unknown.
+static int blocks_per_cu(const void* kern, size_t lds) {
+  static std::mutex mu;
+  static std::map<const void*, int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(kern);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kTlNWV * 64, lds) != hipSuccess || n < 1) n = 1;
+  cache[kern] = n;
+  return n;
+}
+
+// Feature blocks [0, nbn) of a projection over token blocks of MG groups, as whole rounds of
+// resident blocks where it pays: with nbn * nbm blocks and R resident at once, a last partial
+// round leaves most CUs idle while it runs.  Then the first nbn_main feature blocks (a multiple of
+// whole rounds) keep the block shape, and the remaining ones run on token blocks a quarter as
+// tall (MGT groups), which fill a round of their own about four times faster.
+static int tail_split(int nbn, int nbm, int rounds_of) {
+  if (rounds_of < 1 || nbn * nbm <= rounds_of || (nbn * nbm) % rounds_of == 0) return nbn;
+  int main = nbn;
+  while (main > 0 && (main * nbm) % rounds_of) --main;
+  return main;
+}
+
 template <int WF, int NMAT, int TPW, int MG, int NBB>
-static int launch_tiled(TlParams p, hipStream_t s) {
-  const int nbn = p.N / (kTlNWV * TPW * kTileRows);
+static int launch_tiled_part(TlParams p, int bn0, int nbn, int marks, hipStream_t s) {
   p.nbm = (p.M + MG * 16 - 1) / (MG * 16);
+  p.bn0 = bn0;
+  p.ks = 1;
   const size_t lds = (size_t)3 * MG * 2048;
-  launch_timed(NMAT == 2 ? 0 : 1, tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s,
-               p);
+  launch_timed_part(NMAT == 2 ? 0 : 1, marks, tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, dim3(nbn * p.nbm),
+                    dim3(kTlNWV * 64), lds, s, p);
   return check_launch("tiled_kernel");
+}
+
+// MGT: token groups of the tail launch (MGT == MG: no quarter-height tail).  The down projection
+// (NMAT = 1) takes a K-split tail instead: its tail feature blocks keep their token blocks and
+// split K into ks parts, whose partial tiles meet in the workspace (`part`, part_bytes).  A
+// quarter-height tail re-reads every weight tile once per 16 tokens, which made the 27B down
+// projection at 2048 tokens slower (482 against 418 us).
+template <int WF, int NMAT, int TPW, int MG, int NBB, int MGT>
+static int launch_tiled(TlParams p, int num_cus, hipStream_t s) {
+  const int nbn = p.N / (kTlNWV * TPW * kTileRows);
+  const int nbm = (p.M + MG * 16 - 1) / (MG * 16);
+  p.ks = 1;
+  if constexpr (MGT == MG) {
+    const int per_cu = blocks_per_cu((const void*)tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, (size_t)3 * MG * 2048);
+    const int rounds_of = num_cus * per_cu;
+    const int main = NMAT == 1 && p.part ? tail_split(nbn, nbm, rounds_of) : nbn;
+    const int tail_tiles = (nbn - main) * nbm;
+    const size_t tile_bytes = (size_t)kTlNWV * TPW * MG * 256 * 4;
+    int ks = tail_tiles > 0 ? std::min(std::max(1, rounds_of / tail_tiles), p.C) : 1;
+    while (ks > 1 && (size_t)tail_tiles * ks * tile_bytes > (size_t)p.part_bytes) --ks;
+    if (main == nbn || main == 0 || ks < 2) return launch_tiled_part<WF, NMAT, TPW, MG, NBB>(p, 0, nbn, 3, s);
+    if (int rc = launch_tiled_part<WF, NMAT, TPW, MG, NBB>(p, 0, main, 1, s)) return rc;
+    p.ks = ks;
+    p.nbm = nbm;
+    p.bn0 = main;
+    launch_timed_part(NMAT == 2 ? 0 : 1, 2, tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, dim3(tail_tiles * ks),
+                      dim3(kTlNWV * 64), (size_t)3 * MG * 2048, s, p);
+    return check_launch("tiled_kernel");
+  }
+  const int per_cu = blocks_per_cu((const void*)tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, (size_t)3 * MG * 2048);
+  const int main = tail_split(nbn, nbm, num_cus * per_cu);
+  if (main == nbn || main == 0) return launch_tiled_part<WF, NMAT, TPW, MG, NBB>(p, 0, nbn, 3, s);
+  if (int rc = launch_tiled_part<WF, NMAT, TPW, MG, NBB>(p, 0, main, 1, s)) return rc;
+  return launch_tiled_part<WF, NMAT, TPW, MGT, NBB>(p, main, nbn - main, 2, s);
 }
 
 // 32 x 32 gate/up kernel (block-float weights): 8 waves x 32 features x 4 groups of 32 tokens per
@@ -559,12 +673,24 @@ static int launch_tiled(TlParams p, hipStream_t s) {
 constexpr int kTl32MG = 4;
 
 template <int WF, int MG, int NBB>
-static int launch_tiled32(TlParams p, hipStream_t s) {
-  const int nbn = p.N / (kTlNWV * 2 * kTileRows);
+static int launch_tiled32_part(TlParams p, int bn0, int nbn, int marks, hipStream_t s) {
   p.nbm = (p.M + MG * 32 - 1) / (MG * 32);
+  p.bn0 = bn0;
+  p.ks = 1;
   const size_t lds = (size_t)3 * MG * 4096;
-  launch_timed(0, tiled32_kernel<WF, MG, NBB>, dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s, p);
+  launch_timed_part(0, marks, tiled32_kernel<WF, MG, NBB>, dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s, p);
   return check_launch("tiled32_kernel");
+}
+
+template <int WF, int MG, int NBB>
+static int launch_tiled32(TlParams p, int num_cus, hipStream_t s) {
+  const int nbn = p.N / (kTlNWV * 2 * kTileRows);
+  const int nbm = (p.M + MG * 32 - 1) / (MG * 32);
+  const int per_cu = blocks_per_cu((const void*)tiled32_kernel<WF, MG, NBB>, (size_t)3 * MG * 4096);
+  const int main = tail_split(nbn, nbm, num_cus * per_cu);
+  if (main == nbn || main == 0) return launch_tiled32_part<WF, MG, NBB>(p, 0, nbn, 3, s);
+  if (int rc = launch_tiled32_part<WF, MG, NBB>(p, 0, main, 1, s)) return rc;
+  return launch_tiled32_part<WF, 1, NBB>(p, main, nbn - main, 2, s);
 }
 
 bool tiled_supported(int M, int H, int I) {
@@ -572,7 +698,6 @@ bool tiled_supported(int M, int H, int I) {
 }
 
 int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
-  (void)num_cus;
   if (!tiled_supported(a.M, a.H, a.I)) return set_error(-1, "tiled path: H=%d I=%d not multiples of 256", a.H, a.I);
   const WsLayout L = ws_layout(a.M, a.H, a.I, a.fmt);
   const int fmt = a.fmt;
@@ -598,9 +723,9 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.tout = th;
   g.out = h;
   constexpr int GT = kTlGuTPW, GM = kTlGuMG, DT = kTlDnTPW, DM = kTlDnMG;
-  int rc = fmt == 2   ? launch_tiled32<2, kTl32MG, 3>(g, s)
-           : fmt == 1 ? launch_tiled32<1, kTl32MG, 2>(g, s)
-                      : launch_tiled<0, 2, GT, GM, 2>(g, s);
+  int rc = fmt == 2   ? launch_tiled32<2, kTl32MG, 3>(g, num_cus, s)
+           : fmt == 1 ? launch_tiled32<1, kTl32MG, 2>(g, num_cus, s)
+                      : launch_tiled<0, 2, GT, GM, 2, GM / 4>(g, num_cus, s);
   if (rc) return rc;
   TlParams d{};
   d.w0 = a.wd;
@@ -616,7 +741,11 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.residual = a.residual;
   d.out_f32 = a.out_f32;
   d.res_f32 = a.res_f32;
-  rc = dfmt == 1 ? launch_tiled<1, 1, DT, DM, 2>(d, s) : launch_tiled<0, 1, DT, DM, 3>(d, s);
+  // the K-split tail's partial tiles: x16 and xn (adjacent, read only by the gate/up projection)
+  d.part = (float*)(a.ws + L.x16);
+  d.part_bytes = (int)std::min<size_t>(L.total - L.x16, (size_t)1 << 30);
+  d.counters = (int*)(a.ws + L.counters_d);
+  rc = dfmt == 1 ? launch_tiled<1, 1, DT, DM, 2, DM>(d, num_cus, s) : launch_tiled<0, 1, DT, DM, 3, DM>(d, num_cus, s);
   if (rc) return rc;
   return 0;
 }
