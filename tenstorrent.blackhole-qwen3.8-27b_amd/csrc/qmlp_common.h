@@ -205,13 +205,15 @@ __device__ __forceinline__ void dq16_bf16(u32x4 w, uint32_t ebyte, bf16x8& a0, b
 
 // LDS layout of the matrix-core B operand, 2 KB per 64-K step of 16 token rows.  Lane
 // l = 16 q + rr needs K = 16 q + 8 h + (0..7) of token row rr for its two products (h = 0, 1).
-// The halves live in separate 1 KB blocks and inside a block the lane's 16-byte slot is rotated
-// by 2 q + h: every 16-lane read and the 8 chunks that fill one token row's step land in distinct
-// 16-byte bank groups.  (The hardware counters still report about 4 conflict cycles per read of
-// this layout in the many-token down kernel and none on its stores; they report none for the
-// 32 x 32 kernels' layout.)
+// The halves live in separate 1 KB blocks and inside a block the lane's 16-byte slot is
+// rr ^ (2 q + h), so that the 8 chunks which fill one token row's step land in distinct 16-byte
+// bank groups.  Measured on gfx950 (a probe of 16-byte LDS reads and stores, 16 waves per CU):
+// the 64-lane reads of this layout run at ~222 B/clk per CU, as lane-linear reads do, and the
+// staging stores at ~75 B/clk.  A rotation by 2 q + h instead of the xor halves the read rate
+// (~124 B/clk: lanes 0-15 and 16-31 must address their 256-byte rows alike up to the low two
+// slot bits), and no swizzle at all quarters the store rate (~16 B/clk).
 __host__ __device__ inline uint32_t bfrag_off(int q, int rr, int h) {
-  return (uint32_t)(h * 1024 + (q * 16 + ((rr + 2 * q + h) & 15)) * 16);
+  return (uint32_t)(h * 1024 + (q * 16 + (rr ^ (2 * q + h))) * 16);
 }
 
 // Logical workgroup index so that consecutive logical indices share an XCD (hardware dispatches

@@ -16,8 +16,10 @@
 //
 // Pipeline per 64-K step s: compute step s from LDS slot s%3 and register stage s%3; issue the
 // weight loads of step s+3 into that stage; write the B rows of step s+2 (requested one or three
-// steps earlier, by the number of B register buffers) into slot (s+2)%3; one barrier.  Loads
-// beyond the last step are clamped duplicates, so every load is unconditional.
+// steps earlier, by the number of B register buffers) into slot (s+2)%3; one barrier.  The row
+// exponents of a 256-K superblock (one 32-bit word per lane and tile) are requested once per
+// superblock, a superblock ahead.  Loads beyond the last step are clamped duplicates, so every
+// weight and B load is unconditional.
 //
 // Epilogue (fp32 accumulators in registers): gate/up -> h = silu(g) * u rounded once (fp16 *
 // 2^th for bfp8, bf16 for bf16 weights); down -> out = residual + y.  No cross-workgroup
@@ -50,10 +52,22 @@ struct TlParams {
   int out_f32, res_f32;
 };
 
+// Runs steps s .. nst-1 of a block's K loop, unrolled by U (the period of the register stage and
+// buffer rotation): step(k, s) runs step s, k = s % U (a constant of each unrolled copy).
+template <int U, typename F>
+__device__ __forceinline__ void run_steps(int s, int nst, F&& step) {
+  for (; s + U <= nst; s += U)
+#pragma unroll
+    for (int k = 0; k < U; ++k) step(k, s + k);
+  const int r = nst - s;
+#pragma unroll
+  for (int k = 0; k < U - 1; ++k)
+    if (k < r) step(k, s + k);
+}
+
 template <int WF, int NMAT, int TPW>
 struct TlStage {
   typename StepWord<WF>::type w[NMAT][TPW][WF ? 1 : 2];
-  uint32_t e[NMAT][TPW];
 };
 
 template <int WF, int NMAT, int TPW, int MG, int NWV, int NBB>
@@ -122,12 +136,33 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
       for (int t = 0; t < TPW; ++t) {
         const uint8_t* b = wt[mat][t] + off;
         st.w[mat][t][0] = *(const typename StepWord<WF>::type*)(b + lw);
-        if constexpr (WF) {
-          st.e[mat][t] = *(const uint32_t*)(wt[mat][t] + (uint32_t)(sc >> 2) * BLK + le);
-        } else {
-          st.w[mat][t][1] = *(const u32x4*)(b + 1024 + lw);
-        }
+        if constexpr (!WF) st.w[mat][t][1] = *(const u32x4*)(b + 1024 + lw);
       }
+  };
+  // Row exponents: the lane's 32-bit word of a tile's superblock holds the group exponents of
+  // the superblock's 4 K-steps (byte j: step j), so it is requested once per superblock, one
+  // superblock ahead of its use (ecur: the superblock being computed, enext: the next one).
+  // Requested with every step's weights, it made 2 of the 5 vector memory instructions of a
+  // down-projection step, on kernels bound by their vector memory path.
+  uint32_t ecur[NMAT][TPW], enext[NMAT][TPW];
+  const int nsb = nst / kSteps;
+  auto eload = [&](uint32_t(&e)[NMAT][TPW], int sb) {
+    if constexpr (WF != 0) {
+      const uint32_t off = (uint32_t)(kbase / kSteps + min(sb, nsb - 1)) * BLK + le;
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) e[mat][t] = *(const uint32_t*)(wt[mat][t] + off);
+    }
+  };
+  auto erotate = [&](int sb) {  // after the last step of superblock sb
+    if constexpr (WF != 0) {
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) ecur[mat][t] = enext[mat][t];
+      eload(enext, sb + 2);
+    }
   };
 
   f32x4 acc[NMAT][TPW][MG];
@@ -139,7 +174,8 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
       for (int g = 0; g < MG; ++g) acc[mat][t][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const uint32_t boff0 = bfrag_off(lane >> 4, lane & 15, 0), boff1 = bfrag_off(lane >> 4, lane & 15, 1);
-  auto compute = [&](const TlStage<WF, NMAT, TPW>& st, int step) {
+  // kq = step % 4: the step's byte of the exponent word
+  auto compute = [&](const TlStage<WF, NMAT, TPW>& st, int step, int kq) {
     const uint8_t* slot = lds + (step % 3) * SLOT;
     if constexpr (WF) {
       f16x8 a[NMAT][TPW][2];
@@ -148,10 +184,10 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
 #pragma unroll
         for (int t = 0; t < TPW; ++t) {
           if constexpr (WF == 2)
-            dq16_bf4(st.w[mat][t][0].x, st.w[mat][t][0].y, scale_pair(st.e[mat][t], step & 3), a[mat][t][0],
+            dq16_bf4(st.w[mat][t][0].x, st.w[mat][t][0].y, scale_pair(ecur[mat][t], kq), a[mat][t][0],
                      a[mat][t][1]);
           else
-            dq16(st.w[mat][t][0], scale_pair(st.e[mat][t], step & 3), a[mat][t][0], a[mat][t][1]);
+            dq16(st.w[mat][t][0], scale_pair(ecur[mat][t], kq), a[mat][t][0], a[mat][t][1]);
         }
 #pragma unroll
       for (int g = 0; g < MG; ++g) {
@@ -187,63 +223,54 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   // iterations to land (step s+5 is requested in iteration s, like the weight stages); NBB = 2
   // gives one (step s+3 is requested at the top of iteration s) for the kernels whose occupancy
   // the third buffer's registers would halve.
+  constexpr int U = NBB == 3 ? 3 : 6;
   TlStage<WF, NMAT, TPW> s0, s1, s2;
   u32x4 b0[CPT], b1[CPT], b2[CPT];
   bload(b0, 0);
   bload(b1, 1);
+  eload(ecur, 0);
   wload(s0, 0);
   wload(s1, 1);
   wload(s2, 2);
+  eload(enext, 1);
   bstore(b0, 0);
   bstore(b1, 1);
   bload(b2, 2);
   int s = 0;
+  // iteration k of the unroll: stage k % 3 computes step s and then receives step s+3; after a
+  // superblock's last step (a uniform branch) the exponent words move on
+  auto stage = [&](int i) -> TlStage<WF, NMAT, TPW>& { return i == 0 ? s0 : (i == 1 ? s1 : s2); };
   if constexpr (NBB == 3) {
     bload(b0, 3);
     bload(b1, 4);
     __syncthreads();
     // iteration s: the buffer holding step s+2 goes to LDS slot (s+2) % 3 (last read in
     // iteration s-1) and then receives step s+5.
-    auto iter = [&](TlStage<WF, NMAT, TPW>& cur, u32x4(&bw)[CPT], int s) {
-      compute(cur, s);
+    run_steps<U>(s, nst, [&](int k, int s) {
+      TlStage<WF, NMAT, TPW>& cur = stage(k % 3);
+      u32x4(&bw)[CPT] = k % 3 == 0 ? b2 : (k % 3 == 1 ? b0 : b1);
+      compute(cur, s, s & 3);
       wload(cur, s + 3);
       bstore(bw, s + 2);
       bload(bw, s + 5);
+      if ((s & 3) == 3) erotate(s / kSteps);
       __syncthreads();
-    };
-    for (; s + 3 <= nst; s += 3) {
-      iter(s0, b2, s);
-      iter(s1, b0, s + 1);
-      iter(s2, b1, s + 2);
-    }
-    const int r = nst - s;
-    if (r > 0) iter(s0, b2, s);
-    if (r > 1) iter(s1, b0, s + 1);
+    });
   } else {
     __syncthreads();
     // iteration s: bnext receives step s+3 (it held step s+1, already in LDS); bwrite holds step
     // s+2 and goes to slot (s+2) % 3, which was last read in iteration s-1.
-    auto iter = [&](TlStage<WF, NMAT, TPW>& cur, u32x4(&bnext)[CPT], u32x4(&bwrite)[CPT], int s) {
+    run_steps<U>(s, nst, [&](int k, int s) {
+      TlStage<WF, NMAT, TPW>& cur = stage(k % 3);
+      u32x4(&bnext)[CPT] = k % 2 == 0 ? b1 : b2;
+      u32x4(&bwrite)[CPT] = k % 2 == 0 ? b2 : b1;
       bload(bnext, s + 3);
-      compute(cur, s);
+      compute(cur, s, s & 3);
       wload(cur, s + 3);
       bstore(bwrite, s + 2);
+      if ((s & 3) == 3) erotate(s / kSteps);
       __syncthreads();
-    };
-    for (; s + 6 <= nst; s += 6) {
-      iter(s0, b1, b2, s);
-      iter(s1, b2, b1, s + 1);
-      iter(s2, b1, b2, s + 2);
-      iter(s0, b2, b1, s + 3);
-      iter(s1, b1, b2, s + 4);
-      iter(s2, b2, b1, s + 5);
-    }
-    const int r = nst - s;
-    if (r > 0) iter(s0, b1, b2, s);
-    if (r > 1) iter(s1, b2, b1, s + 1);
-    if (r > 2) iter(s2, b1, b2, s + 2);
-    if (r > 3) iter(s0, b2, b1, s + 3);
-    if (r > 4) iter(s1, b1, b2, s + 4);
+    });
   }
 
   if constexpr (NMAT == 1) {
@@ -364,7 +391,6 @@ __host__ __device__ inline uint32_t b32_slot(int u, int l) {
 template <int WF>
 struct Tl32Stage {
   typename StepWord<WF>::type w[2][WF ? 2 : 4];
-  uint32_t e[2][2];
 };
 
 template <int WF, int MG, int NBB>
@@ -424,14 +450,10 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
       if constexpr (WF == 1) {
         st.w[mat][0] = *(const u32x4*)(b + (sc & 3) * 1024 + lp0 * 16u);
         st.w[mat][1] = *(const u32x4*)(b + (sc & 3) * 1024 + lp1 * 16u);
-        st.e[mat][0] = *(const uint32_t*)(b + 4096 + lp0 * 4u);
-        st.e[mat][1] = *(const uint32_t*)(b + 4096 + lp1 * 4u);
       } else if constexpr (WF == 2) {
         const uint32_t o = (uint32_t)(sc & 2) * 512u + (uint32_t)(sc & 1) * 8u;
         st.w[mat][0] = *(const u32x2*)(b + o + lp0 * 16u);
         st.w[mat][1] = *(const u32x2*)(b + o + lp1 * 16u);
-        st.e[mat][0] = *(const uint32_t*)(b + 2048 + lp0 * 4u);
-        st.e[mat][1] = *(const uint32_t*)(b + 2048 + lp1 * 4u);
       } else {
         const uint8_t* bb = b + (sc & 3) * 2048;
         st.w[mat][0] = *(const u32x4*)(bb + lp0 * 16u);
@@ -439,6 +461,29 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
         st.w[mat][2] = *(const u32x4*)(bb + lp1 * 16u);
         st.w[mat][3] = *(const u32x4*)(bb + 1024 + lp1 * 16u);
       }
+    }
+  };
+
+  // Row exponents, once per superblock and one superblock ahead, as in tiled_kernel: the lane's
+  // words for its rows lp0 and lp1 of each matrix's tile.
+  uint32_t ecur[2][2], enext[2][2];
+  auto eload = [&](uint32_t(&e)[2][2], int sb) {
+    if constexpr (WF != 0) {
+      const uint32_t eo = (uint32_t)min(sb, p.C - 1) * BLK + (WF == 2 ? 2048u : 4096u);
+#pragma unroll
+      for (int mat = 0; mat < 2; ++mat) {
+        e[mat][0] = *(const uint32_t*)(wt[mat] + eo + lp0 * 4u);
+        e[mat][1] = *(const uint32_t*)(wt[mat] + eo + lp1 * 4u);
+      }
+    }
+  };
+  auto erotate = [&](int sb) {  // after the last step of superblock sb
+    if constexpr (WF != 0) {
+#pragma unroll
+      for (int mat = 0; mat < 2; ++mat)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) ecur[mat][c] = enext[mat][c];
+      eload(enext, sb + 2);
     }
   };
 
@@ -453,7 +498,8 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   uint32_t bs[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) bs[u] = b32_slot(u, lane) * 16u;
-  auto compute = [&](const Tl32Stage<WF>& st, int step) {
+  // kq = step % 4: the step's byte of the exponent word
+  auto compute = [&](const Tl32Stage<WF>& st, int step, int kq) {
     const uint8_t* slot = lds + (step % 3) * SLOT;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
@@ -462,9 +508,9 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
 #pragma unroll
         for (int mat = 0; mat < 2; ++mat) {
           if constexpr (WF == 2)
-            dq16_bf4(st.w[mat][c].x, st.w[mat][c].y, scale_pair(st.e[mat][c], step & 3), a[mat][0], a[mat][1]);
+            dq16_bf4(st.w[mat][c].x, st.w[mat][c].y, scale_pair(ecur[mat][c], kq), a[mat][0], a[mat][1]);
           else
-            dq16(st.w[mat][c], scale_pair(st.e[mat][c], step & 3), a[mat][0], a[mat][1]);
+            dq16(st.w[mat][c], scale_pair(ecur[mat][c], kq), a[mat][0], a[mat][1]);
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -493,62 +539,51 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   // The pipeline of tiled_kernel: NBB = 3 B register buffers request step s+5 in iteration s,
   // NBB = 2 request step s+3 at the top of iteration s; weights of step s+3 are requested right
   // after step s's products; one barrier per step.
+  constexpr int U = NBB == 3 ? 3 : 6;
   Tl32Stage<WF> s0, s1, s2;
   u32x4 b0[CPT], b1[CPT], b2[CPT];
   bload(b0, 0);
   bload(b1, 1);
+  eload(ecur, 0);
   wload(s0, 0);
   wload(s1, 1);
   wload(s2, 2);
+  eload(enext, 1);
   bstore(b0, 0);
   bstore(b1, 1);
   bload(b2, 2);
   int s = 0;
+  auto stage = [&](int i) -> Tl32Stage<WF>& { return i == 0 ? s0 : (i == 1 ? s1 : s2); };
   if constexpr (NBB == 3) {
     bload(b0, 3);
     bload(b1, 4);
     __syncthreads();
-    auto iter = [&](Tl32Stage<WF>& cur, u32x4(&bw)[CPT], int s) {
-      compute(cur, s);
+    run_steps<U>(s, nst, [&](int k, int s) {
+      Tl32Stage<WF>& cur = stage(k % 3);
+      u32x4(&bw)[CPT] = k % 3 == 0 ? b2 : (k % 3 == 1 ? b0 : b1);
+      compute(cur, s, s & 3);
       wload(cur, s + 3);
       bstore(bw, s + 2);
       bload(bw, s + 5);
+      if ((s & 3) == 3) erotate(s / kSteps);
       __syncthreads();
-    };
-    for (; s + 3 <= nst; s += 3) {
-      iter(s0, b2, s);
-      iter(s1, b0, s + 1);
-      iter(s2, b1, s + 2);
-    }
-    const int r = nst - s;
-    if (r > 0) iter(s0, b2, s);
-    if (r > 1) iter(s1, b0, s + 1);
+    });
   } else {
     __syncthreads();
-    auto iter = [&](Tl32Stage<WF>& cur, u32x4(&bnext)[CPT], u32x4(&bwrite)[CPT], int s) {
+    run_steps<U>(s, nst, [&](int k, int s) {
+      Tl32Stage<WF>& cur = stage(k % 3);
+      u32x4(&bnext)[CPT] = k % 2 == 0 ? b1 : b2;
+      u32x4(&bwrite)[CPT] = k % 2 == 0 ? b2 : b1;
       bload(bnext, s + 3);
-      compute(cur, s);
+      compute(cur, s, s & 3);
       // keeps the next weight loads behind the products: hoisted above them, their registers
       // make the compiler wait for every LDS read before its two products
       __builtin_amdgcn_sched_barrier(0);
       wload(cur, s + 3);
       bstore(bwrite, s + 2);
+      if ((s & 3) == 3) erotate(s / kSteps);
       __syncthreads();
-    };
-    for (; s + 6 <= nst; s += 6) {
-      iter(s0, b1, b2, s);
-      iter(s1, b2, b1, s + 1);
-      iter(s2, b1, b2, s + 2);
-      iter(s0, b2, b1, s + 3);
-      iter(s1, b1, b2, s + 4);
-      iter(s2, b2, b1, s + 5);
-    }
-    const int r = nst - s;
-    if (r > 0) iter(s0, b1, b2, s);
-    if (r > 1) iter(s1, b2, b1, s + 1);
-    if (r > 2) iter(s2, b1, b2, s + 2);
-    if (r > 3) iter(s0, b2, b1, s + 3);
-    if (r > 4) iter(s1, b1, b2, s + 4);
+    });
   }
 
   // epilogue: accumulator v of lane l holds feature 8 (v / 4) + 4 (l / 32) + v % 4 of the pair

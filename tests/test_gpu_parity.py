@@ -227,6 +227,32 @@ def test_forward_stream_fallback(pkg, cuda, fmt):
         _check(y.cpu().numpy(), _oracle(x.float().cpu().numpy(), hw), f"stream fallback {fmt} M={M}")
 
 
+@pytest.mark.parametrize("H,I,M,want_extra", [(2560, 36864, 32, 4), (4864, 53248, 16, 10), (4864, 24576, 32, 16)])
+def test_forward_wide_gate_up_groups(pkg, cuda, H, I, M, want_extra):
+    """Wide intermediates give gate/up tile groups of more than two tiles per wave (G = 18..26
+    tiles for 8 waves).  The last arrival spreads the (tile, token group) pieces beyond two tiles
+    per wave over the waves, one per wave with its first batch of loads and the rest in later
+    rounds; both paths are checked here (want_extra = pieces beyond 16 tiles)."""
+    import ctypes
+
+    import torch
+    from qwen_mlp_amd import workloads
+
+    out = (ctypes.c_int * 6)()
+    assert pkg.lib().qmlp_plan_split(I, H, 2, M, 256, out) == 0
+    G, mg = out[1], 2 if M > 16 else 1
+    assert (G - 16) * mg == want_extra, list(out)
+    assert pkg.lib().qmlp_plan_split(H, I, 1, M, 256, out) == 0  # the whole forward stays on this kernel
+    print(f"case wide gate/up H={H} I={I} M={M} G={G}", flush=True)
+    sd = workloads.state_dict(H, I, layer=5, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format="bfp8", max_tokens=M)
+    hw = _host_weights(pkg, sd, "bfp8")
+    x = workloads.activations(M, H, seed=4300 + M, device=cuda)
+    y = mlp.forward(x, residual=x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check(y.cpu().numpy(), _oracle(x.float().cpu().numpy(), hw), f"wide gate/up H={H} I={I} M={M}")
+
+
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 def test_zero_input_and_aliasing(pkg, cuda, fmt):
     import torch
