@@ -417,7 +417,7 @@ __device__ __forceinline__ void gepilogue(const GvParams& p, int t, const f32x4 
           g = __builtin_amdgcn_ldexpf(g, (int)e.rexp[0][v]);
           u = __builtin_amdgcn_ldexpf(u, (int)e.rexp[1][v]);
         }
-        const float hv = g / (1.0f + expf(-g)) * u;
+        const float hv = silu_mul(g, u);
         // bf16 weights: h is the bf16 operand of the down projection, rounded once like the
         // reference's fused epilogue; bfp8: fp16 * 2^th (one rounding from fp32).
         o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(hv, th[mg])) : f32_to_bf16(hv);

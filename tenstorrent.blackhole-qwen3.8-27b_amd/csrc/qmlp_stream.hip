@@ -280,7 +280,7 @@ __global__ __launch_bounds__(NW * 64) void stream_kernel(StParams p) {
             gv = __builtin_amdgcn_ldexpf(gv, p.rowexp0[nb + v]);
             uv = __builtin_amdgcn_ldexpf(uv, p.rowexp1[nb + v]);
           }
-          o[v] = f32_to_bf16(gv / (1.0f + expf(-gv)) * uv);
+          o[v] = f32_to_bf16(silu_mul(gv, uv));
         }
         *(u32x2*)((uint16_t*)p.out + (size_t)m * p.N + nb) =
             u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};

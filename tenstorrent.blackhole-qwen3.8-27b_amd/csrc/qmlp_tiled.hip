@@ -326,7 +326,7 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
             gv = __builtin_amdgcn_ldexpf(gv, p.rowexp0[n + v] - ts);
             uv = __builtin_amdgcn_ldexpf(uv, p.rowexp1[n + v] - ts);
           }
-          const float hv = gv / (1.0f + expf(-gv)) * uv;
+          const float hv = silu_mul(gv, uv);
           o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(hv, to)) : f32_to_bf16(hv);
         }
       } else {
@@ -606,7 +606,7 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
           gv = __builtin_amdgcn_ldexpf(gv, p.rowexp0[n + v] - ts);
           uv = __builtin_amdgcn_ldexpf(uv, p.rowexp1[n + v] - ts);
         }
-        const float hv = gv / (1.0f + expf(-gv)) * uv;
+        const float hv = silu_mul(gv, uv);
         o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(hv, to)) : f32_to_bf16(hv);
       }
       *(u32x2*)((uint16_t*)p.out + (size_t)m * p.N + n) =
