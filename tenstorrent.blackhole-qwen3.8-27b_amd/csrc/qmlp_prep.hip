@@ -13,8 +13,11 @@ namespace qmlp {
 //
 // One wave per token row, 16-byte loads (H is a multiple of 256, so a row is a whole number of
 // 16-byte chunks): the first pass reduces the row's max|x| and sum of squares (lane partials, then
-// a fixed xor tree: deterministic), the second re-reads the row (from L2) and writes x16.
-constexpr int kPrepRows = 4;  // token rows (waves) per block
+// a fixed xor tree: deterministic), the second converts and writes x16.  Rows of up to
+// 64 * kPrepRegCh chunks (H <= 8192) are held in registers between the passes, with every load
+// of the row in flight at once; longer rows re-read their chunks (from L2) in the second pass.
+constexpr int kPrepRows = 4;    // token rows (waves) per block
+constexpr int kPrepRegCh = 16;  // 16-byte chunks per lane held in registers
 
 __global__ __launch_bounds__(64 * kPrepRows) void prep_kernel(const uint16_t* __restrict__ x, int M, int H,
                                                              const Trailer* tg, const Trailer* tu,
@@ -25,10 +28,10 @@ __global__ __launch_bounds__(64 * kPrepRows) void prep_kernel(const uint16_t* __
   if (m >= M) return;  // whole waves
   const u32x4* xr = (const u32x4*)(x + (size_t)m * H);
   const int nch = H / 8;
+  const bool in_regs = nch <= 64 * kPrepRegCh;
   float mx = 0.f;
   double ss = 0.0;
-  for (int c = lane; c < nch; c += 64) {
-    const u32x4 v = xr[c];
+  auto reduce = [&](const u32x4& v) {
     float cs = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -38,6 +41,17 @@ __global__ __launch_bounds__(64 * kPrepRows) void prep_kernel(const uint16_t* __
       cs = fmaf(hi, hi, cs);
     }
     ss += (double)cs;
+  };
+  u32x4 rv[kPrepRegCh];
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kPrepRegCh; ++i)
+      if (lane + 64 * i < nch) rv[i] = xr[lane + 64 * i];
+#pragma unroll
+    for (int i = 0; i < kPrepRegCh; ++i)
+      if (lane + 64 * i < nch) reduce(rv[i]);
+  } else {
+    for (int c = lane; c < nch; c += 64) reduce(xr[c]);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -57,8 +71,7 @@ __global__ __launch_bounds__(64 * kPrepRows) void prep_kernel(const uint16_t* __
     th[m] = bound > 0.0 ? 15 - eb : 0;
   }
   u32x4* orow = (u32x4*)(x16 + (size_t)m * H);
-  for (int c = lane; c < nch; c += 64) {
-    const u32x4 v = xr[c];
+  auto convert = [&](const u32x4& v) {
     u32x4 o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -66,7 +79,14 @@ __global__ __launch_bounds__(64 * kPrepRows) void prep_kernel(const uint16_t* __
       o[i] = (uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(lo, txm)) |
              ((uint32_t)f32_to_f16_bits(__builtin_amdgcn_ldexpf(hi, txm)) << 16);
     }
-    orow[c] = o;
+    return o;
+  };
+  if (in_regs) {
+#pragma unroll
+    for (int i = 0; i < kPrepRegCh; ++i)
+      if (lane + 64 * i < nch) orow[lane + 64 * i] = convert(rv[i]);
+  } else {
+    for (int c = lane; c < nch; c += 64) orow[c] = convert(xr[c]);
   }
 }
 
