@@ -40,8 +40,10 @@ struct TlParams {
   const uint16_t* src;   // [M, K] B rows: fp16 * 2^tsrc[m] (bfp8 weights) or bf16
   int M, K, N, C;        // N output features, C = K / 256
   int nbm;               // token blocks
-  int bn0;               // first feature block of this launch
-  int ks;                // down projection: K splits per tile (1: every block covers all of K)
+  int bn0;               // first feature block of the K-split part
+  int ks;                // down projection: K splits per tile of the K-split part (1: no split)
+  int nfull;             // leading blocks that cover whole K ranges of feature blocks 0, 1, ...
+                         // (tiled_kernel; the K-split part follows them in the same launch)
   float* part;           // ks > 1: fp32 partial tiles, [tile][K split][block's outputs]
   int part_bytes;
   int* counters;         // ks > 1: arrival counter per tile (left at zero)
@@ -83,15 +85,23 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int L = xcd_logical(blockIdx.x, gridDim.x);  // blocks sharing weights share an XCD
+  // A launch holds up to two parts: blocks [0, nfull) each cover the whole K range of one tile
+  // of feature blocks 0, 1, ...; the rest split the K range of each tile of feature blocks
+  // bn0, ... into ks parts.  The hardware dispatches blocks in index order as earlier ones
+  // retire, so the short K-split blocks fill the CUs that finish their whole-K blocks first
+  // (on a CU the block dispatched first finishes ~25 % sooner than the second).
+  const bool full = (int)blockIdx.x < p.nfull;
+  const int b = full ? (int)blockIdx.x : (int)blockIdx.x - p.nfull;
+  const int L = xcd_logical(b, full ? p.nfull : (int)gridDim.x - p.nfull);  // blocks sharing weights share an XCD
+  const int ks = full ? 1 : p.ks;
   // tile = (feature block, token block); with K splits, the ks blocks of a tile are consecutive
-  const int tile = L / p.ks, q = L % p.ks;
-  const int bn = p.bn0 + tile / p.nbm, bm = tile % p.nbm;
+  const int tile = L / ks, q = L % ks;
+  const int bn = (full ? 0 : p.bn0) + tile / p.nbm, bm = tile % p.nbm;
   const int m0 = bm * MG * 16;
   const int tile0 = (bn * NWV + wave) * TPW;
   // K range of this block: superblocks [q C / ks, (q + 1) C / ks), steps counted from kbase
-  const int kbase = q * p.C / p.ks * kSteps;
-  const int nst = (q + 1) * p.C / p.ks * kSteps - kbase;
+  const int kbase = q * p.C / ks * kSteps;
+  const int nst = (q + 1) * p.C / ks * kSteps - kbase;
 
   // B chunk c = threadIdx.x + i * NT: token row r = c / 8, 8 K values j = c % 8 of the step;
   // quarter j / 2, half j % 2.  Rows beyond M repeat row M - 1 (their outputs are not stored).
@@ -274,13 +284,13 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   }
 
   if constexpr (NMAT == 1) {
-    if (p.ks > 1) {
+    if (ks > 1) {
       // K-split tail: publish the partial tile, arrive; the last of the tile's ks blocks adds
       // the ks partials in K order (deterministic) and runs the epilogue.
       __shared__ int s_last;
       const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(p.part, 0, p.part_bytes, kBufferRsrcWord3);
       auto slot = [&](int qq, int t, int g) {  // byte offset of this lane's f32x4 in split qq's tile
-        return (uint32_t)(((((size_t)tile * p.ks + qq) * NWV + wave) * TPW * MG + t * MG + g) * 64 + lane) * 16u;
+        return (uint32_t)(((((size_t)tile * ks + qq) * NWV + wave) * TPW * MG + t * MG + g) * 64 + lane) * 16u;
       };
 #pragma unroll
       for (int t = 0; t < TPW; ++t)
@@ -290,7 +300,7 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
       __syncthreads();
       if (threadIdx.x == 0) {
         const int old = __hip_atomic_fetch_add(p.counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = old == p.ks - 1;
+        s_last = old == ks - 1;
         if (s_last) __hip_atomic_store(p.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       __syncthreads();
@@ -300,7 +310,7 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
 #pragma unroll
         for (int g = 0; g < MG; ++g) {
           f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-          for (int qq = 0; qq < p.ks; ++qq) sum += qq == q ? acc[0][t][g] : load_coherent(prs, slot(qq, t, g));
+          for (int qq = 0; qq < ks; ++qq) sum += qq == q ? acc[0][t][g] : load_coherent(prs, slot(qq, t, g));
           acc[0][t][g] = sum;
         }
     }
@@ -661,6 +671,7 @@ static int launch_tiled_part(TlParams p, int bn0, int nbn, int marks, hipStream_
   p.nbm = (p.M + MG * 16 - 1) / (MG * 16);
   p.bn0 = bn0;
   p.ks = 1;
+  p.nfull = 0;
   const size_t lds = (size_t)3 * MG * 2048;
   launch_timed_part(NMAT == 2 ? 0 : 1, marks, tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, dim3(nbn * p.nbm),
                     dim3(kTlNWV * 64), lds, s, p);
@@ -669,9 +680,11 @@ static int launch_tiled_part(TlParams p, int bn0, int nbn, int marks, hipStream_
 
 // MGT: token groups of the tail launch (MGT == MG: no quarter-height tail).  The down projection
 // (NMAT = 1) takes a K-split tail instead: its tail feature blocks keep their token blocks and
-// split K into ks parts, whose partial tiles meet in the workspace (`part`, part_bytes).  A
-// quarter-height tail re-reads every weight tile once per 16 tokens, which made the 27B down
-// projection at 2048 tokens slower (482 against 418 us).
+// split K into ks parts, whose partial tiles meet in the workspace (`part`, part_bytes), and
+// these blocks follow the whole-K blocks in the same launch (`nfull`), so that each starts on
+// the first CU slot to free up instead of after the last whole-K block.  A quarter-height tail
+// re-reads every weight tile once per 16 tokens, which made the 27B down projection at 2048
+// tokens slower (482 against 418 us).
 template <int WF, int NMAT, int TPW, int MG, int NBB, int MGT>
 static int launch_tiled(TlParams p, int num_cus, hipStream_t s) {
   const int nbn = p.N / (kTlNWV * TPW * kTileRows);
@@ -686,12 +699,12 @@ static int launch_tiled(TlParams p, int num_cus, hipStream_t s) {
     int ks = tail_tiles > 0 ? std::min(std::max(1, rounds_of / tail_tiles), p.C) : 1;
     while (ks > 1 && (size_t)tail_tiles * ks * tile_bytes > (size_t)p.part_bytes) --ks;
     if (main == nbn || main == 0 || ks < 2) return launch_tiled_part<WF, NMAT, TPW, MG, NBB>(p, 0, nbn, 3, s);
-    if (int rc = launch_tiled_part<WF, NMAT, TPW, MG, NBB>(p, 0, main, 1, s)) return rc;
     p.ks = ks;
     p.nbm = nbm;
     p.bn0 = main;
-    launch_timed_part(NMAT == 2 ? 0 : 1, 2, tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, dim3(tail_tiles * ks),
-                      dim3(kTlNWV * 64), (size_t)3 * MG * 2048, s, p);
+    p.nfull = main * nbm;
+    launch_timed_part(NMAT == 2 ? 0 : 1, 3, tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>,
+                      dim3(main * nbm + tail_tiles * ks), dim3(kTlNWV * 64), (size_t)3 * MG * 2048, s, p);
     return check_launch("tiled_kernel");
   }
   const int per_cu = blocks_per_cu((const void*)tiled_kernel<WF, NMAT, TPW, MG, kTlNWV, NBB>, (size_t)3 * MG * 2048);
