@@ -361,13 +361,14 @@ def test_shape_errors(pkg, cuda):
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 @pytest.mark.parametrize("H,I,M", [(1024, 3072, 2048), (5120, 17408, 256), (1024, 3072, 200), (1024, 3072, 33),
-                                   (1024, 4352, 2048), (5120, 512, 2048)])
+                                   (1024, 4352, 2048), (5120, 512, 2048), (6144, 2048, 2048)])
 def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
     """Many-token forwards (the LDS-tiled matrix-core kernels): a full 2048-token chunk, the 27B
     shape, a token count that leaves a partial token block, the narrowest width that takes this
-    path (one partial block in each projection), and two shapes whose blocks do not fill whole
-    rounds of the GPU, so that the gate/up (I = 4352) or the down projection (H = 5120) runs its
-    last feature blocks as a second launch on quarter-height token blocks."""
+    path (one partial block in each projection), and shapes whose blocks do not fill whole rounds
+    of the GPU: the gate/up (I = 4352) then runs its last feature blocks as a second launch on
+    quarter-height token blocks, and the down projection (H = 5120 or 6144) splits the K range of
+    its last feature blocks in the same launch (2 ways at K = 512 and at H = 6144, K = 2048)."""
     import torch
     from qwen_mlp_amd import workloads
 
