@@ -422,21 +422,26 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
 
   // B chunk c = threadIdx.x + i * NT: token row r = c / 8, K values 8 k8 .. 8 k8 + 7 of the step
   // (k8 = c % 8 = 4 hk + u).  Rows beyond M repeat row M - 1 (their outputs are not stored).
+  // Every load goes through a buffer descriptor whose base is uniform (the block's token rows,
+  // the wave's pair of weight tiles): the lane's byte offset is a constant 32-bit register and
+  // the step's offset a uniform scalar, so no load needs per-lane 64-bit address arithmetic.
+  const int brows = min(MG * 32, p.M - m0);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint8_t*)p.src + (size_t)m0 * p.K * 2), 0, brows * p.K * 2, kBufferRsrcWord3);
   uint32_t goff[CPT], loff[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = min((int)threadIdx.x, NLD - 1) + i * NLD, r = c >> 3, k8 = c & 7;
-    const int mr = min(m0 + r, p.M - 1);
+    const int mr = min(r, brows - 1);
     goff[i] = (uint32_t)(mr * p.K + k8 * 8) * 2u;
     loff[i] = (uint32_t)(r >> 5) * 4096u + b32_slot(k8 & 3, 32 * (k8 >> 2) + (r & 31)) * 16u;
   }
-  const uint8_t* srcb = (const uint8_t*)p.src;
   const bool loader = NLD == NT || (int)threadIdx.x < NLD;  // whole waves
   auto bload = [&](u32x4(&v)[CPT], int step) {
-    const uint8_t* base = srcb + (size_t)min(step, nst - 1) * 128;
+    const int so = min(step, nst - 1) * 128;
     if (loader)
 #pragma unroll
-      for (int i = 0; i < CPT; ++i) v[i] = *(const u32x4*)(base + goff[i]);
+      for (int i = 0; i < CPT; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, goff[i], so, 0);
   };
   auto bstore = [&](const u32x4(&v)[CPT], int step) {
     uint8_t* slot = lds + (step % 3) * SLOT;
@@ -446,30 +451,33 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   };
 
   const int hk = lane >> 5;
-  const uint8_t* wt[2];
+  const int tile_bytes = p.C * BLK;
+  __amdgpu_buffer_rsrc_t wr[2];  // the wave's two tiles (2 pair, 2 pair + 1) of each matrix
 #pragma unroll
   for (int mat = 0; mat < 2; ++mat)
-    wt[mat] = (mat ? p.w1 : p.w0) + (size_t)(2 * pair + ((lane >> 4) & 1)) * p.C * BLK;
+    wr[mat] = __builtin_amdgcn_make_buffer_rsrc((void*)((mat ? p.w1 : p.w0) + (size_t)(2 * pair) * tile_bytes), 0,
+                                                2 * tile_bytes, kBufferRsrcWord3);
   const uint32_t lp0 = (uint32_t)(32 * hk + (lane & 15)), lp1 = lp0 + 16u;
+  const uint32_t wv = (uint32_t)((lane >> 4) & 1) * (uint32_t)tile_bytes;  // the lane's tile
   auto wload = [&](Tl32Stage<WF>& st, int step) {
     const int sc = min(step, nst - 1);
-    const uint32_t bo = (uint32_t)(sc >> 2) * BLK;
+    const int bo = (sc >> 2) * BLK;
 #pragma unroll
     for (int mat = 0; mat < 2; ++mat) {
-      const uint8_t* b = wt[mat] + bo;
       if constexpr (WF == 1) {
-        st.w[mat][0] = *(const u32x4*)(b + (sc & 3) * 1024 + lp0 * 16u);
-        st.w[mat][1] = *(const u32x4*)(b + (sc & 3) * 1024 + lp1 * 16u);
+        const int so = bo + (sc & 3) * 1024;
+        st.w[mat][0] = __builtin_amdgcn_raw_buffer_load_b128(wr[mat], wv + lp0 * 16u, so, 0);
+        st.w[mat][1] = __builtin_amdgcn_raw_buffer_load_b128(wr[mat], wv + lp1 * 16u, so, 0);
       } else if constexpr (WF == 2) {
-        const uint32_t o = (uint32_t)(sc & 2) * 512u + (uint32_t)(sc & 1) * 8u;
-        st.w[mat][0] = *(const u32x2*)(b + o + lp0 * 16u);
-        st.w[mat][1] = *(const u32x2*)(b + o + lp1 * 16u);
+        const int so = bo + (sc & 2) * 512 + (sc & 1) * 8;
+        st.w[mat][0] = __builtin_amdgcn_raw_buffer_load_b64(wr[mat], wv + lp0 * 16u, so, 0);
+        st.w[mat][1] = __builtin_amdgcn_raw_buffer_load_b64(wr[mat], wv + lp1 * 16u, so, 0);
       } else {
-        const uint8_t* bb = b + (sc & 3) * 2048;
-        st.w[mat][0] = *(const u32x4*)(bb + lp0 * 16u);
-        st.w[mat][1] = *(const u32x4*)(bb + 1024 + lp0 * 16u);
-        st.w[mat][2] = *(const u32x4*)(bb + lp1 * 16u);
-        st.w[mat][3] = *(const u32x4*)(bb + 1024 + lp1 * 16u);
+        const int so = bo + (sc & 3) * 2048;
+        st.w[mat][0] = __builtin_amdgcn_raw_buffer_load_b128(wr[mat], wv + lp0 * 16u, so, 0);
+        st.w[mat][1] = __builtin_amdgcn_raw_buffer_load_b128(wr[mat], wv + 1024u + lp0 * 16u, so, 0);
+        st.w[mat][2] = __builtin_amdgcn_raw_buffer_load_b128(wr[mat], wv + lp1 * 16u, so, 0);
+        st.w[mat][3] = __builtin_amdgcn_raw_buffer_load_b128(wr[mat], wv + 1024u + lp1 * 16u, so, 0);
       }
     }
   };
@@ -479,11 +487,11 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   uint32_t ecur[2][2], enext[2][2];
   auto eload = [&](uint32_t(&e)[2][2], int sb) {
     if constexpr (WF != 0) {
-      const uint32_t eo = (uint32_t)min(sb, p.C - 1) * BLK + (WF == 2 ? 2048u : 4096u);
+      const int so = min(sb, p.C - 1) * BLK + (WF == 2 ? 2048 : 4096);
 #pragma unroll
       for (int mat = 0; mat < 2; ++mat) {
-        e[mat][0] = *(const uint32_t*)(wt[mat] + eo + lp0 * 4u);
-        e[mat][1] = *(const uint32_t*)(wt[mat] + eo + lp1 * 4u);
+        e[mat][0] = __builtin_amdgcn_raw_buffer_load_b32(wr[mat], wv + lp0 * 4u, so, 0);
+        e[mat][1] = __builtin_amdgcn_raw_buffer_load_b32(wr[mat], wv + lp1 * 4u, so, 0);
       }
     }
   };
