@@ -105,21 +105,26 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
 
   // B chunk c = threadIdx.x + i * NT: token row r = c / 8, 8 K values j = c % 8 of the step;
   // quarter j / 2, half j % 2.  Rows beyond M repeat row M - 1 (their outputs are not stored).
+  // Every load goes through a buffer descriptor whose base is uniform (the block's token rows,
+  // the wave's weight tiles): the lane's byte offset is a constant 32-bit register and the
+  // step's offset a uniform scalar, so no load needs per-lane 64-bit address arithmetic.
+  const int brows = min(MG * 16, p.M - m0);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint8_t*)p.src + (size_t)m0 * p.K * 2), 0, brows * p.K * 2, kBufferRsrcWord3);
   uint32_t goff[CPT], loff[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = min((int)threadIdx.x, NLD - 1) + i * NLD, r = c >> 3, j = c & 7;
-    const int mr = min(m0 + r, p.M - 1);
+    const int mr = min(r, brows - 1);
     goff[i] = (uint32_t)(mr * p.K + j * 8) * 2u;
     loff[i] = (uint32_t)(r >> 4) * 2048u + bfrag_off(j >> 1, r & 15, j & 1);
   }
-  const uint8_t* srcb = (const uint8_t*)p.src;
   const bool loader = NLD == NT || (int)threadIdx.x < NLD;  // whole waves
   auto bload = [&](u32x4(&v)[CPT], int step) {
-    const uint8_t* base = srcb + (size_t)(kbase + min(step, nst - 1)) * 128;
+    const int so = (kbase + min(step, nst - 1)) * 128;
     if (loader)
 #pragma unroll
-      for (int i = 0; i < CPT; ++i) v[i] = *(const u32x4*)(base + goff[i]);
+      for (int i = 0; i < CPT; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, goff[i], so, 0);
   };
   auto bstore = [&](const u32x4(&v)[CPT], int step) {
     uint8_t* slot = lds + (step % 3) * SLOT;
@@ -128,25 +133,29 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
       for (int i = 0; i < CPT; ++i) *(u32x4*)(slot + loff[i]) = v[i];
   };
 
-  const uint8_t* wt[NMAT][TPW];
+  const int tile_bytes = p.C * BLK;
+  __amdgpu_buffer_rsrc_t wr[NMAT];  // the wave's TPW tiles of each matrix
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-    for (int t = 0; t < TPW; ++t) wt[mat][t] = (mat ? p.w1 : p.w0) + (size_t)(tile0 + t) * p.C * BLK;
+    wr[mat] = __builtin_amdgcn_make_buffer_rsrc((void*)((mat ? p.w1 : p.w0) + (size_t)tile0 * tile_bytes), 0,
+                                                TPW * tile_bytes, kBufferRsrcWord3);
   const uint32_t lw = (uint32_t)lane * 16u, le = (WF == 2 ? 2048u : 4096u) + (uint32_t)lane * 4u;
   // Weights are re-read by every token block of the same features, so they are loaded with the
   // default cache policy (kept in L2 for the neighbouring blocks of the XCD).
   auto wload = [&](TlStage<WF, NMAT, TPW>& st, int step) {
     const int sc = kbase + min(step, nst - 1);  // kbase is a multiple of 4: sc & 3 == step & 3
-    const uint32_t off = (uint32_t)(sc >> 2) * BLK +
-                         (WF == 2 ? (uint32_t)(sc & 2) * 512u + (uint32_t)(sc & 1) * 8u : (uint32_t)(sc & 3) * SB);
+    const int so = (sc >> 2) * BLK + (WF == 2 ? (sc & 2) * 512 + (sc & 1) * 8 : (sc & 3) * SB);
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
-        const uint8_t* b = wt[mat][t] + off;
-        st.w[mat][t][0] = *(const typename StepWord<WF>::type*)(b + lw);
-        if constexpr (!WF) st.w[mat][t][1] = *(const u32x4*)(b + 1024 + lw);
+        const uint32_t vo = (uint32_t)(t * tile_bytes) + lw;
+        if constexpr (WF == 2) {
+          st.w[mat][t][0] = __builtin_amdgcn_raw_buffer_load_b64(wr[mat], vo, so, 0);
+        } else {
+          st.w[mat][t][0] = __builtin_amdgcn_raw_buffer_load_b128(wr[mat], vo, so, 0);
+          if constexpr (!WF) st.w[mat][t][1] = __builtin_amdgcn_raw_buffer_load_b128(wr[mat], vo + 1024u, so, 0);
+        }
       }
   };
   // Row exponents: the lane's 32-bit word of a tile's superblock holds the group exponents of
@@ -158,11 +167,12 @@ __global__ __launch_bounds__(NWV * 64) void tiled_kernel(TlParams p) {
   const int nsb = nst / kSteps;
   auto eload = [&](uint32_t(&e)[NMAT][TPW], int sb) {
     if constexpr (WF != 0) {
-      const uint32_t off = (uint32_t)(kbase / kSteps + min(sb, nsb - 1)) * BLK + le;
+      const int so = (kbase / kSteps + min(sb, nsb - 1)) * BLK;
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) e[mat][t] = *(const uint32_t*)(wt[mat][t] + off);
+        for (int t = 0; t < TPW; ++t)
+          e[mat][t] = __builtin_amdgcn_raw_buffer_load_b32(wr[mat], (uint32_t)(t * tile_bytes) + le, so, 0);
     }
   };
   auto erotate = [&](int sb) {  // after the last step of superblock sb
