@@ -654,8 +654,8 @@ constexpr int kTlNWV = 8;  // waves per block
 //   down:    2 tiles per wave x 4 groups (256 features x 64 tokens): 415-423 us, against 535-542
 //            us for 1 tile x 8 groups, 488-492 us for 4 tiles x 4 groups, 424-437 us for 5.
 // B register buffers (NBB): 3 where the registers allow two blocks per CU anyway or one block
-// regardless (gate/up bfp8 704-707 us against 711-723; bf16 down 445 against 514 us); 2 for the
-// bfp8 down projection, which keeps two blocks per CU only under 128 VGPRs (420 against 519 us).
+// regardless (gate/up bfp8 704-707 us against 711-723; bf16 down 445 against 514 us; the bfp8
+// down projection at 118 VGPRs once its loads went through buffer descriptors, 377 against 378).
 constexpr int kTlGuTPW = 1, kTlGuMG = 8;
 constexpr int kTlDnTPW = 2, kTlDnMG = 4;
 
@@ -811,7 +811,7 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.part = (float*)(a.ws + L.x16);
   d.part_bytes = (int)std::min<size_t>(L.total - L.x16, (size_t)1 << 30);
   d.counters = (int*)(a.ws + L.counters_d);
-  rc = dfmt == 1 ? launch_tiled<1, 1, DT, DM, 2, DM>(d, num_cus, s) : launch_tiled<0, 1, DT, DM, 3, DM>(d, num_cus, s);
+  rc = dfmt == 1 ? launch_tiled<1, 1, DT, DM, 3, DM>(d, num_cus, s) : launch_tiled<0, 1, DT, DM, 3, DM>(d, num_cus, s);
   if (rc) return rc;
   return 0;
 }
