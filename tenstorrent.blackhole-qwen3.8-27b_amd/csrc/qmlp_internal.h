@@ -73,6 +73,7 @@ struct WsLayout {
   size_t part_gu, part_d;          // fp32 partial-sum slots
   size_t pss;                      // per-workgroup token sums of squares
   size_t xn;                       // bf16 [M, H] normalised activations (RMSNorm pass)
+  size_t split, split_bytes;       // partial tiles of the many-token 32x32 kernels' K splits
   size_t total;
 };
 WsLayout ws_layout(int M, int H, int I, int fmt);
@@ -100,6 +101,10 @@ int launch_prep(const ForwardArgs& a, hipStream_t s);
 int launch_rmsnorm(const void* x, const void* w, float eps, int M, int H, void* xn, hipStream_t s);
 int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s);
 bool tiled_supported(int M, int H, int I);
+// Workspace bytes for the partial tiles of the 32x32 many-token kernels' K-split pieces (0 where
+// neither projection of the shape splits on kSplitMaxSlots resident blocks).
+constexpr int kSplitMaxSlots = 256;
+size_t tiled_split_bytes(int M, int H, int I, int fmt);
 int launch_forward_gemv(const ForwardArgs& a, int num_cus, hipStream_t s);
 // Stream-K weight-streaming kernels for M <= 32 (qmlp_stream.hip).
 int plan_stream(int rows, int K, int num_cus, int* P, int* maxseg);

@@ -26,6 +26,7 @@
 // reduction: every output element is owned by one lane of one wave.
 #include <map>
 #include <mutex>
+#include <type_traits>
 
 #include "qmlp_common.h"
 #include "qmlp_internal.h"
@@ -46,7 +47,8 @@ struct TlParams {
                          // (tiled_kernel; the K-split part follows them in the same launch)
   float* part;           // ks > 1: fp32 partial tiles, [tile][K split][block's outputs]
   int part_bytes;
-  int* counters;         // ks > 1: arrival counter per tile (left at zero)
+  int* counters;         // ks > 1: arrival counter per tile (tiled_kernel), publication counter
+                         // per split tile (tiled32_kernel); left at zero
   const int* tsrc;       // bfp8: per-token exponent of src
   const int* tout;       // bfp8 gate/up: h16 = h * 2^tout[m]
   void* out;             // gate/up: h [M, N] 16-bit; down: out [M, N] bf16 or fp32
@@ -408,12 +410,24 @@ __host__ __device__ inline uint32_t b32_slot(int u, int l) {
   return (uint32_t)(u * 64 + (l & ~7) + ((l + 2 * u + (l >> 5)) & 7));
 }
 
-template <int WF>
+template <int WF, int NM>
 struct Tl32Stage {
-  typename StepWord<WF>::type w[2][WF ? 2 : 4];
+  typename StepWord<WF>::type w[NM][WF ? 2 : 4];
 };
 
-template <int WF, int MG, int NBB>
+constexpr int kSplitMaxPieces = 4;  // K pieces per split tile of tiled32_kernel
+
+// NM = 2: gate/up (the wave's 32-row feature pair of both matrices); NM = 1: the down projection
+// (one 32-row unit of its matrix per wave, residual epilogue).
+//
+// Work: blocks [0, nfull) each take one whole tile (tile = the block's logical index, feature
+// blocks from bn0); blocks from nfull take K pieces of the tiles that follow: ks consecutive
+// blocks share a tile, piece q covering superblocks [q C / ks, (q + 1) C / ks).  The whole tiles
+// come in complete rounds of resident blocks and the pieces start together as those rounds end,
+// so the blocks reading one feature block's weights read the same K range at the same time (L2
+// reuse).  A split tile's pieces meet through the workspace: pieces 0 .. ks-2 publish their
+// partial tiles, piece ks-1 adds them in K order and runs the epilogue.
+template <int WF, int MG, int NBB, int NM>
 __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   constexpr int NWV = 8, NT = NWV * 64;
   constexpr int SLOT = MG * 4096;     // LDS bytes of one 64-K step of B
@@ -421,20 +435,52 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   constexpr int CPT = (MG * 256 + NT - 1) / NT, NLD = MG * 256 / CPT;
   static_assert(CPT * NLD == MG * 256 && NLD <= NT && NLD % 64 == 0, "B chunks must divide evenly over whole waves");
   constexpr int BLK = WF == 2 ? kBf4Block : (WF ? kBfp8Block : kBf16Block);
+  constexpr uint32_t PART_BYTES = NWV * NM * MG * 16 * 64 * 4;  // one piece's partial tile
   extern __shared__ __align__(16) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int L = xcd_logical(blockIdx.x, gridDim.x);  // blocks sharing weights share an XCD
-  const int bn = p.bn0 + L / p.nbm, bm = L % p.nbm;
+  const bool full = (int)blockIdx.x < p.nfull;
+  const int b = full ? (int)blockIdx.x : (int)blockIdx.x - p.nfull;
+  const int ks = full ? 1 : p.ks;
+  // blocks sharing weights share an XCD; the pieces of a split tile keep their order (piece
+  // ks - 1 has the highest block index of its tile), which needs ks to divide the part's blocks
+  // per XCD
+  const int P = full ? p.nfull : (int)gridDim.x - p.nfull;
+  const int L = full || (P / 8) % ks == 0 ? xcd_logical(b, P) : b;
+  const int tt = L / ks, q = L % ks;  // split tiles: index among them, piece
+  const int tile = full ? L : p.nfull + tt;
+  const int bn = p.bn0 + tile / p.nbm, bm = tile % p.nbm;
   const int m0 = bm * MG * 32;
-  const int pair = bn * NWV + wave;
-  const int nst = p.C * kSteps;
+  const int pair = bn * NWV + wave;  // the wave's 32-row unit (of each matrix)
+  const int k0 = q * p.C / ks, nsb = (q + 1) * p.C / ks - k0;  // the piece's superblocks
+  const int kb = k0 * kSteps, nst = nsb * kSteps;
+
+  // The epilogue's exponents (the block's NM x 256 row exponents, its 128 tokens' exponents)
+  // staged in LDS after the B ring: requested first, written to LDS before the first barrier, read
+  // after the last.  Kept out of the epilogue's global loads, which could not pass its stores.
+  int* lexp = (int*)(lds + 3 * SLOT);  // [NM][NWV * 32] row exponents, then [2][MG * 32] token ones
+  constexpr int NEXP = WF ? NM * NWV * 32 + (NM == 2 ? 2 : 1) * MG * 32 : 0;
+  static_assert(NEXP <= 2 * NT, "two exponents per thread at most");
+  int xval[2] = {0, 0};
+  if constexpr (WF != 0) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int i = (int)threadIdx.x + r * NT;
+      if (i < NM * NWV * 32) {
+        const int* re = i < NWV * 32 ? p.rowexp0 : p.rowexp1;
+        xval[r] = re[bn * NWV * 32 + (i & (NWV * 32 - 1))];
+      } else if (i < NEXP) {
+        const int j = i - NM * NWV * 32, mm = min(m0 + (j & (MG * 32 - 1)), p.M - 1);
+        xval[r] = j < MG * 32 ? p.tsrc[mm] : p.tout[mm];
+      }
+    }
+  }
 
   // B chunk c = threadIdx.x + i * NT: token row r = c / 8, K values 8 k8 .. 8 k8 + 7 of the step
   // (k8 = c % 8 = 4 hk + u).  Rows beyond M repeat row M - 1 (their outputs are not stored).
   // Every load goes through a buffer descriptor whose base is uniform (the block's token rows,
-  // the wave's pair of weight tiles): the lane's byte offset is a constant 32-bit register and
-  // the step's offset a uniform scalar, so no load needs per-lane 64-bit address arithmetic.
+  // the wave's weight tiles): the lane's byte offset is a constant 32-bit register and the step's
+  // offset a uniform scalar, so no load needs per-lane 64-bit address arithmetic.
   const int brows = min(MG * 32, p.M - m0);
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((const uint8_t*)p.src + (size_t)m0 * p.K * 2), 0, brows * p.K * 2, kBufferRsrcWord3);
@@ -447,8 +493,36 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     loff[i] = (uint32_t)(r >> 5) * 4096u + b32_slot(k8 & 3, 32 * (k8 >> 2) + (r & 31)) * 16u;
   }
   const bool loader = NLD == NT || (int)threadIdx.x < NLD;  // whole waves
+
+  // Down projection: the residual words of the lane's outputs (group g, rows 8 vq + 0..3 of its
+  // 4-row quarter), requested before the K loop by the block that runs the epilogue, so that
+  // the epilogue issues no global load.  bf16: the low two words; fp32: all four.
+  u32x4 rres[NM == 1 ? MG : 1][4];
+  if constexpr (NM == 1) {
+    const int col = lane & 31, rq = (lane >> 5) * 4;
+#pragma unroll
+    for (int g = 0; g < MG; ++g)
+#pragma unroll
+      for (int vq = 0; vq < 4; ++vq) rres[g][vq] = u32x4{0u, 0u, 0u, 0u};
+    if (p.residual && q == ks - 1) {
+#pragma unroll
+      for (int g = 0; g < MG; ++g) {
+        const size_t row = (size_t)min(m0 + g * 32 + col, p.M - 1) * p.N;
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          const int n = pair * 32 + vq * 8 + rq;
+          if (p.res_f32) {
+            rres[g][vq] = *(const u32x4*)((const float*)p.residual + row + n);
+          } else {
+            const u32x2 w = *(const u32x2*)((const uint16_t*)p.residual + row + n);
+            rres[g][vq] = u32x4{w.x, w.y, 0u, 0u};
+          }
+        }
+      }
+    }
+  }
   auto bload = [&](u32x4(&v)[CPT], int step) {
-    const int so = min(step, nst - 1) * 128;
+    const int so = (kb + min(step, nst - 1)) * 128;
     if (loader)
 #pragma unroll
       for (int i = 0; i < CPT; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, goff[i], so, 0);
@@ -462,18 +536,18 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
 
   const int hk = lane >> 5;
   const int tile_bytes = p.C * BLK;
-  __amdgpu_buffer_rsrc_t wr[2];  // the wave's two tiles (2 pair, 2 pair + 1) of each matrix
+  __amdgpu_buffer_rsrc_t wr[NM];  // the wave's two 16-row tiles (2 pair, 2 pair + 1) of each matrix
 #pragma unroll
-  for (int mat = 0; mat < 2; ++mat)
+  for (int mat = 0; mat < NM; ++mat)
     wr[mat] = __builtin_amdgcn_make_buffer_rsrc((void*)((mat ? p.w1 : p.w0) + (size_t)(2 * pair) * tile_bytes), 0,
                                                 2 * tile_bytes, kBufferRsrcWord3);
   const uint32_t lp0 = (uint32_t)(32 * hk + (lane & 15)), lp1 = lp0 + 16u;
   const uint32_t wv = (uint32_t)((lane >> 4) & 1) * (uint32_t)tile_bytes;  // the lane's tile
-  auto wload = [&](Tl32Stage<WF>& st, int step) {
-    const int sc = min(step, nst - 1);
+  auto wload = [&](Tl32Stage<WF, NM>& st, int step) {
+    const int sc = kb + min(step, nst - 1);
     const int bo = (sc >> 2) * BLK;
 #pragma unroll
-    for (int mat = 0; mat < 2; ++mat) {
+    for (int mat = 0; mat < NM; ++mat) {
       if constexpr (WF == 1) {
         const int so = bo + (sc & 3) * 1024;
         st.w[mat][0] = __builtin_amdgcn_raw_buffer_load_b128(wr[mat], wv + lp0 * 16u, so, 0);
@@ -494,30 +568,30 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
 
   // Row exponents, once per superblock and one superblock ahead, as in tiled_kernel: the lane's
   // words for its rows lp0 and lp1 of each matrix's tile.
-  uint32_t ecur[2][2], enext[2][2];
-  auto eload = [&](uint32_t(&e)[2][2], int sb) {
+  uint32_t ecur[NM][2], enext[NM][2];
+  auto eload = [&](uint32_t(&e)[NM][2], int sb) {
     if constexpr (WF != 0) {
-      const int so = min(sb, p.C - 1) * BLK + (WF == 2 ? 2048 : 4096);
+      const int so = (k0 + min(sb, nsb - 1)) * BLK + (WF == 2 ? 2048 : 4096);
 #pragma unroll
-      for (int mat = 0; mat < 2; ++mat) {
+      for (int mat = 0; mat < NM; ++mat) {
         e[mat][0] = __builtin_amdgcn_raw_buffer_load_b32(wr[mat], wv + lp0 * 4u, so, 0);
         e[mat][1] = __builtin_amdgcn_raw_buffer_load_b32(wr[mat], wv + lp1 * 4u, so, 0);
       }
     }
   };
-  auto erotate = [&](int sb) {  // after the last step of superblock sb
+  auto erotate = [&](int sb) {  // after the last step of the piece's superblock sb
     if constexpr (WF != 0) {
 #pragma unroll
-      for (int mat = 0; mat < 2; ++mat)
+      for (int mat = 0; mat < NM; ++mat)
 #pragma unroll
         for (int c = 0; c < 2; ++c) ecur[mat][c] = enext[mat][c];
       eload(enext, sb + 2);
     }
   };
 
-  f32x16 acc[2][MG];
+  f32x16 acc[NM][MG];
 #pragma unroll
-  for (int mat = 0; mat < 2; ++mat)
+  for (int mat = 0; mat < NM; ++mat)
 #pragma unroll
     for (int g = 0; g < MG; ++g)
 #pragma unroll
@@ -527,14 +601,14 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
 #pragma unroll
   for (int u = 0; u < 4; ++u) bs[u] = b32_slot(u, lane) * 16u;
   // kq = step % 4: the step's byte of the exponent word
-  auto compute = [&](const Tl32Stage<WF>& st, int step, int kq) {
+  auto compute = [&](const Tl32Stage<WF, NM>& st, int step, int kq) {
     const uint8_t* slot = lds + (step % 3) * SLOT;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       if constexpr (WF) {
-        f16x8 a[2][2];
+        f16x8 a[NM][2];
 #pragma unroll
-        for (int mat = 0; mat < 2; ++mat) {
+        for (int mat = 0; mat < NM; ++mat) {
           if constexpr (WF == 2)
             dq16_bf4(st.w[mat][c].x, st.w[mat][c].y, scale_pair(ecur[mat][c], kq), a[mat][0], a[mat][1]);
           else
@@ -546,7 +620,7 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
           for (int g = 0; g < MG; ++g) {
             const f16x8 b = __builtin_bit_cast(f16x8, *(const u32x4*)(slot + g * 4096 + bs[2 * c + h]));
 #pragma unroll
-            for (int mat = 0; mat < 2; ++mat)
+            for (int mat = 0; mat < NM; ++mat)
               acc[mat][g] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mat][h], b, acc[mat][g], 0, 0, 0);
           }
       } else {
@@ -556,7 +630,7 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
           for (int g = 0; g < MG; ++g) {
             const bf16x8 b = __builtin_bit_cast(bf16x8, *(const u32x4*)(slot + g * 4096 + bs[2 * c + h]));
 #pragma unroll
-            for (int mat = 0; mat < 2; ++mat)
+            for (int mat = 0; mat < NM; ++mat)
               acc[mat][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, st.w[mat][2 * c + h]),
                                                                     b, acc[mat][g], 0, 0, 0);
           }
@@ -568,7 +642,7 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   // NBB = 2 request step s+3 at the top of iteration s; weights of step s+3 are requested right
   // after step s's products; one barrier per step.
   constexpr int U = NBB == 3 ? 3 : 6;
-  Tl32Stage<WF> s0, s1, s2;
+  Tl32Stage<WF, NM> s0, s1, s2;
   u32x4 b0[CPT], b1[CPT], b2[CPT];
   bload(b0, 0);
   bload(b1, 1);
@@ -581,13 +655,17 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   bstore(b1, 1);
   bload(b2, 2);
   int s = 0;
-  auto stage = [&](int i) -> Tl32Stage<WF>& { return i == 0 ? s0 : (i == 1 ? s1 : s2); };
+  auto stage = [&](int i) -> Tl32Stage<WF, NM>& { return i == 0 ? s0 : (i == 1 ? s1 : s2); };
+  if constexpr (WF != 0)
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      if ((int)threadIdx.x + r * NT < NEXP) lexp[threadIdx.x + r * NT] = xval[r];
   if constexpr (NBB == 3) {
     bload(b0, 3);
     bload(b1, 4);
     __syncthreads();
     run_steps<U>(s, nst, [&](int k, int s) {
-      Tl32Stage<WF>& cur = stage(k % 3);
+      Tl32Stage<WF, NM>& cur = stage(k % 3);
       u32x4(&bw)[CPT] = k % 3 == 0 ? b2 : (k % 3 == 1 ? b0 : b1);
       compute(cur, s, s & 3);
       wload(cur, s + 3);
@@ -599,7 +677,7 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   } else {
     __syncthreads();
     run_steps<U>(s, nst, [&](int k, int s) {
-      Tl32Stage<WF>& cur = stage(k % 3);
+      Tl32Stage<WF, NM>& cur = stage(k % 3);
       u32x4(&bnext)[CPT] = k % 2 == 0 ? b1 : b2;
       u32x4(&bwrite)[CPT] = k % 2 == 0 ? b2 : b1;
       bload(bnext, s + 3);
@@ -614,33 +692,130 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     });
   }
 
-  // epilogue: accumulator v of lane l holds feature 8 (v / 4) + 4 (l / 32) + v % 4 of the pair
-  // for token l % 32 of each group
-  const int col = lane & 31, rq = (lane >> 5) * 4;
+  // Epilogue over the tile's outputs, one group of 32 tokens at a time: every value the group
+  // needs (its accumulator chunks, partial tiles, residual words) is requested before any of its
+  // stores, so each group costs one memory round trip.  chunk(mat, g, v4) gives accumulators
+  // 4 v4 .. 4 v4 + 3 of matrix mat and group g.  Accumulator v of lane l holds row
+  // 8 (v / 4) + 4 (l / 32) + v % 4 of the wave's 32-row unit for token l % 32 of the group.
+  auto epilogue = [&](auto chunk) {
+    const int col = lane & 31, rq = (lane >> 5) * 4;
+    const int* lrow = lexp + wave * 32 + rq;    // this lane's rows: + 8 vq + v (+ NWV * 32 for up)
+    const int* ltok = lexp + NM * NWV * 32 + col;  // this lane's token: + 32 g (+ MG * 32: tout)
 #pragma unroll
-  for (int g = 0; g < MG; ++g) {
-    const int m = m0 + g * 32 + col;
-    if (m >= p.M) continue;
-    const int ts = WF ? p.tsrc[m] : 0;
-    const int to = WF ? p.tout[m] : 0;
+    for (int g = 0; g < MG; ++g) {
+      const int m = m0 + g * 32 + col;
+      const bool live = m < p.M;
+      f32x4 a[NM][4];
 #pragma unroll
-    for (int vq = 0; vq < 4; ++vq) {
-      const int n = pair * 32 + vq * 8 + rq;
-      uint16_t o[4];
+      for (int mat = 0; mat < NM; ++mat)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        float gv = acc[0][g][4 * vq + v], uv = acc[1][g][4 * vq + v];
-        if constexpr (WF) {
-          gv = __builtin_amdgcn_ldexpf(gv, p.rowexp0[n + v] - ts);
-          uv = __builtin_amdgcn_ldexpf(uv, p.rowexp1[n + v] - ts);
+        for (int vq = 0; vq < 4; ++vq) a[mat][vq] = chunk(mat, g, vq);
+      const int ts = WF ? ltok[32 * g] : 0;
+      if constexpr (NM == 1) {
+        // down: out = residual + y, y = acc * 2^(row exponent - token exponent)
+        if (!live) continue;
+        f32x4 rr[4];
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          const u32x4 w = rres[NM == 1 ? g : 0][vq];
+          rr[vq] = p.res_f32 ? __builtin_bit_cast(f32x4, w)
+                             : f32x4{bf16_to_f32((uint16_t)(w.x & 0xffffu)), bf16_to_f32((uint16_t)(w.x >> 16)),
+                                     bf16_to_f32((uint16_t)(w.y & 0xffffu)), bf16_to_f32((uint16_t)(w.y >> 16))};
         }
-        const float hv = silu_mul(gv, uv);
-        o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(hv, to)) : f32_to_bf16(hv);
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          const int n = pair * 32 + vq * 8 + rq;
+          float y[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            y[v] = (WF ? __builtin_amdgcn_ldexpf(a[0][vq][v], lrow[8 * vq + v] - ts) : a[0][vq][v]) + rr[vq][v];
+          if (p.out_f32) {
+            *(f32x4*)((float*)p.out + (size_t)m * p.N + n) = f32x4{y[0], y[1], y[2], y[3]};
+          } else {
+            const uint32_t o0 = f32_to_bf16(y[0]), o1 = f32_to_bf16(y[1]), o2 = f32_to_bf16(y[2]),
+                           o3 = f32_to_bf16(y[3]);
+            *(u32x2*)((uint16_t*)p.out + (size_t)m * p.N + n) = u32x2{o0 | (o1 << 16), o2 | (o3 << 16)};
+          }
+        }
+      } else {
+        // gate/up: h = silu(g) * u, rounded once
+        if (!live) continue;
+        const int to = WF ? ltok[MG * 32 + 32 * g] : 0;
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          const int n = pair * 32 + vq * 8 + rq;
+          uint16_t o[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            float gv = a[0][vq][v], uv = a[NM - 1][vq][v];
+            if constexpr (WF) {
+              gv = __builtin_amdgcn_ldexpf(gv, lrow[8 * vq + v] - ts);
+              uv = __builtin_amdgcn_ldexpf(uv, lrow[NWV * 32 + 8 * vq + v] - ts);
+            }
+            const float hv = silu_mul(gv, uv);
+            o[v] = WF ? f32_to_f16_bits(__builtin_amdgcn_ldexpf(hv, to)) : f32_to_bf16(hv);
+          }
+          *(u32x2*)((uint16_t*)p.out + (size_t)m * p.N + n) =
+              u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+        }
       }
-      *(u32x2*)((uint16_t*)p.out + (size_t)m * p.N + n) =
-          u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
     }
+  };
+  auto own = [&](int mat, int g, int v4) {
+    return f32x4{acc[mat][g][4 * v4], acc[mat][g][4 * v4 + 1], acc[mat][g][4 * v4 + 2], acc[mat][g][4 * v4 + 3]};
+  };
+  if (ks == 1) {
+    epilogue(own);
+    return;
   }
+
+  // Split tile: pieces 0 .. ks-2 store their partial tile in slot (tt, q) and count themselves
+  // published; piece ks-1, the tile's last block in dispatch order (so the others are resident
+  // or done when it runs, and its wait cannot be held up), waits for the ks-1 publications, adds
+  // the partials in K order, its own last (p_0 + p_1 + ... + p_{ks-1}: deterministic), runs the
+  // epilogue and leaves the counter at zero.
+  int* published = p.counters + tt;
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(p.part, 0, p.part_bytes, kBufferRsrcWord3);
+  auto off = [&](int qq, int mat, int g, int v4) {  // byte offset of this lane's chunk in piece qq's slot
+    return (uint32_t)(tt * ks + qq) * PART_BYTES + (uint32_t)((((wave * NM + mat) * MG + g) * 4 + v4) * 64 + lane) * 16u;
+  };
+  if (q < ks - 1) {
+#pragma unroll
+    for (int mat = 0; mat < NM; ++mat)
+#pragma unroll
+      for (int g = 0; g < MG; ++g)
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) store_coherent(prs, off(q, mat, g, v4), own(mat, g, v4));
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(published, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  if (threadIdx.x == 0) {
+    while (__hip_atomic_load(published, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ks - 1)
+      __builtin_amdgcn_s_sleep(2);
+    __hip_atomic_store(published, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  auto fold = [&](auto ksc) {  // every chunk's ks - 1 loads issued unconditionally
+    constexpr int KS = decltype(ksc)::value;
+    epilogue([&](int mat, int g, int v4) {
+      f32x4 v[KS - 1];
+#pragma unroll
+      for (int r = 0; r < KS - 1; ++r) v[r] = load_coherent(prs, off(r, mat, g, v4));
+      f32x4 sum = v[0];
+#pragma unroll
+      for (int r = 1; r < KS - 1; ++r) sum += v[r];
+      return sum + own(mat, g, v4);
+    });
+  };
+  static_assert(kSplitMaxPieces == 4, "fold instances");
+  if (ks == 2)
+    fold(std::integral_constant<int, 2>{});
+  else if (ks == 3)
+    fold(std::integral_constant<int, 3>{});
+  else
+    fold(std::integral_constant<int, 4>{});
 }
 
 // ---------------------------------------------------------------- host side
@@ -738,25 +913,93 @@ static int launch_tiled(TlParams p, int num_cus, hipStream_t s) {
 // bf16 weights stay on tiled_kernel (846-857 us here: the A stages spill).
 constexpr int kTl32MG = 4;
 
-template <int WF, int MG, int NBB>
-static int launch_tiled32_part(TlParams p, int bn0, int nbn, int marks, hipStream_t s) {
-  p.nbm = (p.M + MG * 32 - 1) / (MG * 32);
+// Bytes of one K piece's partial tile of tiled32_kernel (8 waves x NM 32-row units x MG groups of
+// 32 tokens, fp32).
+constexpr size_t split_part_bytes(int NM, int MG) { return (size_t)kTlNWV * NM * MG * 16 * 64 * 4; }
+
+// Whole rounds plus K-split pieces for a tiled32 projection of ntiles tiles of C superblocks on
+// `slots` resident blocks: the first rounds x slots tiles run whole; the remaining ntail tiles
+// split K into ks <= kSplitMaxPieces pieces with ntail x ks <= slots, so that the pieces fill at
+// most one more round.  ks = 1 (no split) where there is no whole round or no remainder, where
+// fewer than two pieces per tile fit, or where the workspace region does not hold the pieces'
+// partial tiles.
+struct SplitPlan {
+  int nfull, ntail, ks;
+};
+static SplitPlan split_plan(int ntiles, int C, int slots, size_t part_bytes, size_t piece_bytes) {
+  const SplitPlan none{ntiles, 0, 1};
+  if (slots < 1) return none;
+  const int rounds = ntiles / slots, ntail = ntiles - rounds * slots;
+  if (rounds == 0 || ntail == 0 || 2 * (long long)ntail > kMaxDim / kTileRows) return none;
+  int ks = std::min(std::min(slots / ntail, C), kSplitMaxPieces);
+  while (ks > 1 && (size_t)ntail * ks * piece_bytes > part_bytes) --ks;
+  if (ks < 2) return none;
+  return {rounds * slots, ntail, ks};
+}
+
+// Sized for kSplitMaxSlots resident blocks (one per CU of a 256-CU device); split_plan checks the
+// size against the device's own count at launch.
+size_t tiled_split_bytes(int M, int H, int I, int fmt) {
+  if (fmt == 0 || M <= 32) return 0;  // bf16 weights, or no many-token kernels
+  const long long nbm = (M + kTl32MG * 32 - 1) / (kTl32MG * 32), tile_features = kTlNWV * 2 * kTileRows;
+  size_t need = 0;
+  auto add = [&](long long ntiles, int C, size_t piece) {
+    if (ntiles > (1 << 30)) return;
+    const SplitPlan sp = split_plan((int)ntiles, C, kSplitMaxSlots, ~(size_t)0, piece);
+    if (sp.ks > 1) need = std::max(need, (size_t)sp.ntail * sp.ks * piece);
+  };
+  add(I / tile_features * nbm, H / kSuperK, split_part_bytes(2, kTl32MG));
+  add(H / tile_features * nbm, I / kSuperK, split_part_bytes(1, kTl32MG));
+  return need;
+}
+
+// LDS of tiled32_kernel: the 3-slot B ring and the exponent staging area.
+constexpr size_t tiled32_lds(int MG, int NM) { return (size_t)3 * MG * 4096 + (size_t)(NM * 256 + 2 * MG * 32) * 4; }
+
+template <int WF, int MG, int NBB, int NM>
+static int launch_tiled32_plan(TlParams p, int bn0, int nbm, const SplitPlan& sp, int slot, int marks,
+                               hipStream_t s) {
+  p.nbm = nbm;
   p.bn0 = bn0;
-  p.ks = 1;
-  const size_t lds = (size_t)3 * MG * 4096;
-  launch_timed_part(0, marks, tiled32_kernel<WF, MG, NBB>, dim3(nbn * p.nbm), dim3(kTlNWV * 64), lds, s, p);
+  p.nfull = sp.nfull;
+  p.ks = sp.ks;
+  const size_t lds = tiled32_lds(MG, NM);
+  launch_timed_part(slot, marks, tiled32_kernel<WF, MG, NBB, NM>, dim3(sp.nfull + sp.ntail * sp.ks),
+                    dim3(kTlNWV * 64), lds, s, p);
   return check_launch("tiled32_kernel");
 }
 
+// Gate/up: whole rounds plus K-split pieces in one launch where split_plan allows, else whole
+// rounds of one tile per block plus a quarter-height tail launch.
 template <int WF, int MG, int NBB>
 static int launch_tiled32(TlParams p, int num_cus, hipStream_t s) {
   const int nbn = p.N / (kTlNWV * 2 * kTileRows);
   const int nbm = (p.M + MG * 32 - 1) / (MG * 32);
-  const int per_cu = blocks_per_cu((const void*)tiled32_kernel<WF, MG, NBB>, (size_t)3 * MG * 4096);
-  const int main = tail_split(nbn, nbm, num_cus * per_cu);
-  if (main == nbn || main == 0) return launch_tiled32_part<WF, MG, NBB>(p, 0, nbn, 3, s);
-  if (int rc = launch_tiled32_part<WF, MG, NBB>(p, 0, main, 1, s)) return rc;
-  return launch_tiled32_part<WF, 1, NBB>(p, main, nbn - main, 2, s);
+  const int slots = num_cus * blocks_per_cu((const void*)tiled32_kernel<WF, MG, NBB, 2>, tiled32_lds(MG, 2));
+  const SplitPlan sp =
+      p.part ? split_plan(nbn * nbm, p.C, slots, (size_t)p.part_bytes, split_part_bytes(2, MG)) : SplitPlan{0, 0, 1};
+  if (sp.ks > 1) return launch_tiled32_plan<WF, MG, NBB, 2>(p, 0, nbm, sp, 0, 3, s);
+  const int main = tail_split(nbn, nbm, slots);
+  if (main == nbn || main == 0) return launch_tiled32_plan<WF, MG, NBB, 2>(p, 0, nbm, {nbn * nbm, 0, 1}, 0, 3, s);
+  if (int rc = launch_tiled32_plan<WF, MG, NBB, 2>(p, 0, nbm, {main * nbm, 0, 1}, 0, 1, s)) return rc;
+  const int nbm1 = (p.M + 31) / 32;
+  return launch_tiled32_plan<WF, 1, NBB, 2>(p, main, nbm1, {(nbn - main) * nbm1, 0, 1}, 0, 2, s);
+}
+
+// bfp8 down projection on tiled32_kernel (NM = 1): each wave owns one 32-row unit x 4 groups of 32
+// tokens, a block 256 features x 128 tokens, as whole rounds plus K-split pieces.  Returns 1
+// (nothing launched) where that plan has no whole round or no split: then tiled_kernel runs the
+// projection.
+static int launch_down32(TlParams p, int num_cus, hipStream_t s) {
+  constexpr int MG = kTl32MG, NBB = 3;
+  if (p.N % (kTlNWV * 2 * kTileRows)) return 1;
+  const int nbn = p.N / (kTlNWV * 2 * kTileRows), nbm = (p.M + MG * 32 - 1) / (MG * 32);
+  const int slots = num_cus * blocks_per_cu((const void*)tiled32_kernel<1, MG, NBB, 1>, tiled32_lds(MG, 1));
+  const int ntiles = nbn * nbm;
+  SplitPlan sp = p.part ? split_plan(ntiles, p.C, slots, (size_t)p.part_bytes, split_part_bytes(1, MG))
+                        : SplitPlan{ntiles, 0, 1};
+  if (sp.ks == 1 && !(ntiles >= slots && ntiles % slots == 0)) return 1;
+  return launch_tiled32_plan<1, MG, NBB, 1>(p, 0, nbm, sp, 1, 3, s);
 }
 
 bool tiled_supported(int M, int H, int I) {
@@ -788,6 +1031,11 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.tsrc = tx;
   g.tout = th;
   g.out = h;
+  // partial tiles of the 32x32 kernels' K-split pieces: the region at xn (read only before the
+  // gate/up projection, by the activation prep)
+  g.part = L.split_bytes ? (float*)(a.ws + L.split) : nullptr;
+  g.part_bytes = (int)std::min<size_t>(L.split_bytes, (size_t)1 << 30);
+  g.counters = (int*)(a.ws + L.counters_gu);
   constexpr int GT = kTlGuTPW, GM = kTlGuMG, DT = kTlDnTPW, DM = kTlDnMG;
   int rc = fmt == 2   ? launch_tiled32<2, kTl32MG, 3>(g, num_cus, s)
            : fmt == 1 ? launch_tiled32<1, kTl32MG, 2>(g, num_cus, s)
@@ -811,6 +1059,14 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   d.part = (float*)(a.ws + L.x16);
   d.part_bytes = (int)std::min<size_t>(L.total - L.x16, (size_t)1 << 30);
   d.counters = (int*)(a.ws + L.counters_d);
+  if (dfmt == 1) {
+    TlParams d32 = d;
+    d32.part = L.split_bytes ? (float*)(a.ws + L.split) : nullptr;
+    d32.part_bytes = (int)std::min<size_t>(L.split_bytes, (size_t)1 << 30);
+    d32.counters = (int*)(a.ws + L.counters_d);
+    rc = launch_down32(d32, num_cus, s);
+    if (rc != 1) return rc;
+  }
   rc = dfmt == 1 ? launch_tiled<1, 1, DT, DM, 3, DM>(d, num_cus, s) : launch_tiled<0, 1, DT, DM, 3, DM>(d, num_cus, s);
   if (rc) return rc;
   return 0;

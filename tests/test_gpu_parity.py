@@ -361,14 +361,16 @@ def test_shape_errors(pkg, cuda):
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 @pytest.mark.parametrize("H,I,M", [(1024, 3072, 2048), (5120, 17408, 256), (1024, 3072, 200), (1024, 3072, 33),
-                                   (1024, 4352, 2048), (5120, 512, 2048), (6144, 2048, 2048)])
+                                   (1024, 4352, 2048), (5120, 512, 2048), (6144, 2048, 2048), (5376, 2048, 2048),
+                                   (1024, 41728, 160)])
 def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
     """Many-token forwards (the LDS-tiled matrix-core kernels): a full 2048-token chunk, the 27B
-    shape, a token count that leaves a partial token block, the narrowest width that takes this
-    path (one partial block in each projection), and shapes whose blocks do not fill whole rounds
-    of the GPU: the gate/up (I = 4352) then runs its last feature blocks as a second launch on
-    quarter-height token blocks, and the down projection (H = 5120 or 6144) splits the K range of
-    its last feature blocks in the same launch (2 ways at K = 512 and at H = 6144, K = 2048)."""
+    shape at 256 tokens, a token count that leaves a partial token block, the narrowest width that
+    takes this path (one partial block in each projection), and, for the block-float formats,
+    shapes whose tiles do not fill whole rounds of a 256-CU GPU, so that the tiles beyond the last
+    whole round split their K range into pieces that meet in the workspace: gate/up at I = 4352
+    (16 tiles in 4 pieces) and I = 41728 (70 tiles in 3 pieces, block order left as is), down at
+    H = 5120, K = 512 and H = 6144 (2 pieces) and at H = 5376 (80 tiles in 3 pieces)."""
     import torch
     from qwen_mlp_amd import workloads
 
