@@ -22,8 +22,10 @@
 // weight and B load is unconditional.
 //
 // Epilogue (fp32 accumulators in registers): gate/up -> h = silu(g) * u rounded once (fp16 *
-// 2^th for bfp8, bf16 for bf16 weights); down -> out = residual + y.  No cross-workgroup
-// reduction: every output element is owned by one lane of one wave.
+// 2^th for bfp8, bf16 for bf16 weights); down -> out = residual + y.  Every output element is
+// owned by one lane of one wave, except in the tiles that follow the last whole round of resident
+// blocks: those split their K range over a few blocks, whose fp32 partial tiles meet in the
+// workspace and are added in K order by one of them (deterministic).
 #include <map>
 #include <mutex>
 #include <type_traits>
@@ -495,16 +497,19 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   const bool loader = NLD == NT || (int)threadIdx.x < NLD;  // whole waves
 
   // Down projection: the residual words of the lane's outputs (group g, rows 8 vq + 0..3 of its
-  // 4-row quarter), requested before the K loop by the block that runs the epilogue, so that
-  // the epilogue issues no global load.  bf16: the low two words; fp32: all four.
+  // 4-row quarter), requested together after the K loop (by the last piece of a split tile
+  // before its wait), so that they cost one round trip and none of the epilogue's loads waits
+  // behind its stores.  Requested before the loop instead, their completion held up the loop's
+  // first in-order waits (+5 us per block).  bf16: the low two words; fp32: all four.
   u32x4 rres[NM == 1 ? MG : 1][4];
-  if constexpr (NM == 1) {
-    const int col = lane & 31, rq = (lane >> 5) * 4;
 #pragma unroll
-    for (int g = 0; g < MG; ++g)
+  for (int g = 0; g < (NM == 1 ? MG : 1); ++g)
 #pragma unroll
-      for (int vq = 0; vq < 4; ++vq) rres[g][vq] = u32x4{0u, 0u, 0u, 0u};
-    if (p.residual && q == ks - 1) {
+    for (int vq = 0; vq < 4; ++vq) rres[g][vq] = u32x4{0u, 0u, 0u, 0u};
+  auto rload = [&]() {
+    if constexpr (NM == 1) {
+      if (!p.residual || q != ks - 1) return;
+      const int col = lane & 31, rq = (lane >> 5) * 4;
 #pragma unroll
       for (int g = 0; g < MG; ++g) {
         const size_t row = (size_t)min(m0 + g * 32 + col, p.M - 1) * p.N;
@@ -520,7 +525,8 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
         }
       }
     }
-  }
+  };
+
   auto bload = [&](u32x4(&v)[CPT], int step) {
     const int so = (kb + min(step, nst - 1)) * 128;
     if (loader)
@@ -765,6 +771,7 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     return f32x4{acc[mat][g][4 * v4], acc[mat][g][4 * v4 + 1], acc[mat][g][4 * v4 + 2], acc[mat][g][4 * v4 + 3]};
   };
   if (ks == 1) {
+    rload();
     epilogue(own);
     return;
   }
@@ -791,6 +798,7 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     if (threadIdx.x == 0) __hip_atomic_fetch_add(published, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
+  rload();
   if (threadIdx.x == 0) {
     while (__hip_atomic_load(published, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ks - 1)
       __builtin_amdgcn_s_sleep(2);
