@@ -945,20 +945,17 @@ static SplitPlan split_plan(int ntiles, int C, int slots, size_t part_bytes, siz
   return {rounds * slots, ntail, ks};
 }
 
-// Sized for kSplitMaxSlots resident blocks (one per CU of a 256-CU device); split_plan checks the
-// size against the device's own count at launch.
+// Sized for the most any split can hold on kSplitMaxSlots resident blocks (one per CU of a 256-CU
+// device), as soon as either projection has more tiles than that (the first M that can split):
+// constant beyond, so that the workspace never shrinks as M grows (the plan's own need does:
+// 64 tail tiles at 2048 tokens, none at 2049).  split_plan checks the size against the device's
+// own block count at launch.
 size_t tiled_split_bytes(int M, int H, int I, int fmt) {
   if (fmt == 0 || M <= 32) return 0;  // bf16 weights, or no many-token kernels
   const long long nbm = (M + kTl32MG * 32 - 1) / (kTl32MG * 32), tile_features = kTlNWV * 2 * kTileRows;
-  size_t need = 0;
-  auto add = [&](long long ntiles, int C, size_t piece) {
-    if (ntiles > (1 << 30)) return;
-    const SplitPlan sp = split_plan((int)ntiles, C, kSplitMaxSlots, ~(size_t)0, piece);
-    if (sp.ks > 1) need = std::max(need, (size_t)sp.ntail * sp.ks * piece);
-  };
-  add(I / tile_features * nbm, H / kSuperK, split_part_bytes(2, kTl32MG));
-  add(H / tile_features * nbm, I / kSuperK, split_part_bytes(1, kTl32MG));
-  return need;
+  const long long tiles = std::max(I / tile_features, H / tile_features) * nbm;
+  if (tiles <= kSplitMaxSlots) return 0;
+  return (size_t)kSplitMaxSlots * std::max(split_part_bytes(2, kTl32MG), split_part_bytes(1, kTl32MG));
 }
 
 // LDS of tiled32_kernel: the 3-slot B ring and the exponent staging area.

@@ -68,9 +68,10 @@ def test_workspace_bytes(pkg):
 def test_workspace_bytes_never_shrink_as_m_grows(pkg, H, I, fmt):
     """A workspace sized for M tokens serves every call with fewer tokens: the size is
     non-decreasing in M (the split kernels' partial slots at M <= 32 can exceed what 33..~400
-    tokens need otherwise)."""
+    tokens need otherwise, and the many-token kernels' K-split pieces need room at 2048 tokens
+    but none at 2049)."""
     lib = pkg.lib()
-    Ms = list(range(1, 65)) + [100, 200, 373, 374, 512, 1024, 2048]
+    Ms = list(range(1, 4353)) + [6144, 8191, 8192, 8193, 16384, 65536]
     sizes = [lib.qmlp_workspace_bytes(M, H, I, fmt) for M in Ms]
     assert all(s > 0 for s in sizes)
     for (m0, s0), (m1, s1) in zip(zip(Ms, sizes), zip(Ms[1:], sizes[1:])):
