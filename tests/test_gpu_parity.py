@@ -388,6 +388,34 @@ def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
+def test_fp32_residual_stream(pkg, cuda, fmt):
+    """An fp32 residual stream (out = residual + MLP(x), the residual read as fp32) at every kind of
+    dispatch: the weight-streaming kernel (16 tokens), the 16x16 tiled kernels (200 tokens), and at
+    2048 tokens the 32x32 kernel's down projection whose last tiles split K into pieces (block-float
+    formats; bf16 weights take the 16x16 kernel there too); then in place (out = residual)."""
+    import torch
+    from qwen_mlp_amd import workloads
+
+    H, I = 6144, 2048
+    sd = workloads.state_dict(H, I, layer=21, device=cuda)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=2048)
+    hw = _host_weights(pkg, sd, fmt)
+    for M in (16, 200, 2048):
+        print(f"case fp32 residual {fmt} M={M}", flush=True)
+        x = workloads.activations(M, H, seed=7100 + M, gain=False, device=cuda)
+        res = workloads.activations(M, H, seed=7200 + M, gain=False, device=cuda).float() * 3.0 + 0.125
+        ref = omlp.swiglu(x.float().cpu().numpy(), hw["gate_proj"], hw["up_proj"], hw["down_proj"],
+                          residual=res.cpu().numpy())
+        y = mlp.forward(x, residual=res, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        _check(y.cpu().numpy(), ref, f"fp32 residual {fmt} M={M}")
+        r2 = res.clone()
+        mlp.forward(x, residual=r2, out=r2, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(r2, y), f"{fmt} M={M}: in-place fp32 residual differs"
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 def test_rmsnorm_prologue(pkg, cuda, fmt):
     """h + MLP(rmsnorm(h) * (1 + w)) against the oracle's composition (the norm output rounded to
     bf16 as the reference's separate norm produces it), across every dispatch width: fused into
