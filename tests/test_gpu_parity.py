@@ -362,11 +362,14 @@ def test_shape_errors(pkg, cuda):
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
 @pytest.mark.parametrize("H,I,M", [(1024, 3072, 2048), (5120, 17408, 256), (1024, 3072, 200), (1024, 3072, 33),
                                    (1024, 4352, 2048), (5120, 512, 2048), (6144, 2048, 2048), (5376, 2048, 2048),
-                                   (1024, 41728, 160)])
+                                   (1024, 41728, 160), (1024, 3072, 2049), (2048, 2048, 4100)])
 def test_prefill_tiled(pkg, cuda, fmt, H, I, M):
     """Many-token forwards (the LDS-tiled matrix-core kernels): a full 2048-token chunk, the 27B
     shape at 256 tokens, a token count that leaves a partial token block, the narrowest width that
-    takes this path (one partial block in each projection), and, for the block-float formats,
+    takes this path (one partial block in each projection), chunks longer than 2048 tokens with a
+    ragged last block (2049: 204 gate/up tiles, fewer than one round; 4100: 264 tiles in each
+    projection, one whole round and 8 tiles in 4 pieces that meet in the workspace's fixed-size
+    split region), and, for the block-float formats,
     shapes whose tiles do not fill whole rounds of a 256-CU GPU, so that the tiles beyond the last
     whole round split their K range into pieces that meet in the workspace: gate/up at I = 4352
     (16 tiles in 4 pieces) and I = 41728 (70 tiles in 3 pieces, block order left as is), down at
