@@ -1,6 +1,6 @@
 """GPU parity at the full configured sizes, on heavy-tailed data, and against poisoned buffers.
 
-* The 27B prefill chunk (M = 2048, every weight format).  MLP rows are independent, so a fixed
+* The 27B prefill chunk (M = 2048, every weight format; bfp8 also behind the RMSNorm pass).  MLP rows are independent, so a fixed
   sample of token rows is checked against the oracle: the first, middle and last row of every
   64-token block.  The bf16 output must equal the fp32 output rounded once over the whole tensor.
   The reference checks its 2048-row prefill gate/up against native bits
@@ -63,6 +63,29 @@ def test_prefill_27b_m2048_sampled_rows(pkg, cuda, fmt):
     ref = oracle(xf, hw)
     check(y32.cpu().numpy()[rows], ref, f"prefill 27B M={M} {fmt} ({len(rows)} sampled rows)")
     check_bf16(y16.float().cpu().numpy()[rows], ref, f"prefill 27B M={M} {fmt}")
+
+
+def test_rmsnorm_prologue_27b_m2048_sampled_rows(pkg, cuda):
+    """The decoder's feed-forward half at the 27B prefill size: h + MLP(bf16(rmsnorm(h))) with
+    the norm as its own pass before the tiled kernels, on the sampled rows of every 64-token
+    block (h at a residual-stream scale, a norm weight of +-0.3)."""
+    import torch
+    from qwen_mlp_amd import workloads
+
+    M = 2048
+    print(f"case rmsnorm prefill 27B M={M} bfp8", flush=True)
+    sd = workloads.state_dict(H27, I27, layer=11, device=cuda)
+    nw = (torch.randn(H27, generator=torch.Generator(cuda).manual_seed(6), device=cuda) * 0.3).to(torch.bfloat16)
+    h = (workloads.activations(M, H27, seed=78, device=cuda).float() * 30.0).to(torch.bfloat16)
+    mlp = pkg.Qwen36MLP(cuda, sd, weight_format="bfp8", max_tokens=M)
+    y = mlp.forward_rmsnorm(h, nw, eps=1e-6, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y).all())
+    rows = _sample_rows(M)
+    hw = host_weights(pkg, sd, "bfp8")
+    ref = omlp.norm_swiglu(h.float().cpu().numpy()[rows], nw.float().cpu().numpy(), hw["gate_proj"],
+                           hw["up_proj"], hw["down_proj"], 1e-6)
+    check(y.cpu().numpy()[rows], ref, f"rmsnorm prefill 27B M={M} bfp8 ({len(rows)} sampled rows)")
 
 
 # ---------------------------------------------------------------- 64-layer stack
