@@ -25,7 +25,7 @@
 // 2^th for bfp8, bf16 for bf16 weights); down -> out = residual + y.  Every output element is
 // owned by one lane of one wave, except in the tiles that follow the last whole round of resident
 // blocks: those split their K range over a few blocks, whose fp32 partial tiles meet in the
-// workspace and are added in K order by one of them (deterministic).
+// workspace and are added in a fixed order (deterministic), each token group by one block.
 #include <map>
 #include <mutex>
 #include <type_traits>
@@ -427,8 +427,10 @@ constexpr int kSplitMaxPieces = 4;  // K pieces per split tile of tiled32_kernel
 // blocks share a tile, piece q covering superblocks [q C / ks, (q + 1) C / ks).  The whole tiles
 // come in complete rounds of resident blocks and the pieces start together as those rounds end,
 // so the blocks reading one feature block's weights read the same K range at the same time (L2
-// reuse).  A split tile's pieces meet through the workspace: pieces 0 .. ks-2 publish their
-// partial tiles, piece ks-1 adds them in K order and runs the epilogue.
+// reuse).  A split tile's pieces meet through the workspace: where they share an XCD each piece
+// finishes a share of the tile's token groups (it publishes the others' groups, then adds the
+// other pieces' partials of its own); elsewhere pieces 0 .. ks-2 publish their partial tiles and
+// piece ks-1 adds them in K order and runs the epilogue.
 template <int WF, int MG, int NBB, int NM>
 __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   constexpr int NWV = 8, NT = NWV * 64;
@@ -455,6 +457,13 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   const int m0 = bm * MG * 32;
   const int pair = bn * NWV + wave;  // the wave's 32-row unit (of each matrix)
   const int k0 = q * p.C / ks, nsb = (q + 1) * p.C / ks - k0;  // the piece's superblocks
+  // A split tile whose pieces share an XCD (consecutive in its dispatch order) is finished by all
+  // of them, each the token groups g with g % ks == q (gmask); otherwise by its last piece.
+  const bool dist = !full && P % 8 == 0 && (P / 8) % ks == 0 && ks <= MG;
+  uint32_t gmask = 0;
+#pragma unroll
+  for (int g = 0; g < MG; ++g)
+    if (ks == 1 || !dist || g % ks == q) gmask |= 1u << g;
   const int kb = k0 * kSteps, nst = nsb * kSteps;
 
   // The epilogue's exponents (the block's NM x 256 row exponents, its 128 tokens' exponents)
@@ -508,10 +517,11 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     for (int vq = 0; vq < 4; ++vq) rres[g][vq] = u32x4{0u, 0u, 0u, 0u};
   auto rload = [&]() {
     if constexpr (NM == 1) {
-      if (!p.residual || q != ks - 1) return;
+      if (!p.residual || (!dist && q != ks - 1)) return;
       const int col = lane & 31, rq = (lane >> 5) * 4;
 #pragma unroll
       for (int g = 0; g < MG; ++g) {
+        if (!((gmask >> g) & 1u)) continue;
         const size_t row = (size_t)min(m0 + g * 32 + col, p.M - 1) * p.N;
 #pragma unroll
         for (int vq = 0; vq < 4; ++vq) {
@@ -709,6 +719,7 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     const int* ltok = lexp + NM * NWV * 32 + col;  // this lane's token: + 32 g (+ MG * 32: tout)
 #pragma unroll
     for (int g = 0; g < MG; ++g) {
+      if (!((gmask >> g) & 1u)) continue;  // a group another piece of a split tile finishes
       const int m = m0 + g * 32 + col;
       const bool live = m < p.M;
       f32x4 a[NM][4];
@@ -776,41 +787,57 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     return;
   }
 
-  // Split tile: pieces 0 .. ks-2 store their partial tile in slot (tt, q) and count themselves
-  // published; piece ks-1, the tile's last block in dispatch order (so the others are resident
-  // or done when it runs, and its wait cannot be held up), waits for the ks-1 publications, adds
-  // the partials in K order, its own last (p_0 + p_1 + ... + p_{ks-1}: deterministic), runs the
-  // epilogue and leaves the counter at zero.
+  // Split tile.  Every piece publishes, in its slot (tt, q), the groups it does not finish and
+  // counts itself published.
+  // * dist (the pieces share an XCD and are consecutive in its dispatch order, so all of them
+  //   become resident: the XCD dispatches in order and holds more blocks than a tile has
+  //   pieces): each piece waits for all ks publications, adds the other pieces' partials of its
+  //   own groups in K order and its own last (deterministic per group), and runs the epilogue on
+  //   those groups.  Each piece counts itself once more after its wait; the last of those
+  //   leaves the counter at zero.
+  // * otherwise piece ks-1, the tile's last block in dispatch order (the others are resident or
+  //   done when it runs, so its wait cannot be held up), waits for the ks-1 publications of the
+  //   whole partial tiles, adds them in K order, its own last (p_0 + ... + p_{ks-1}), runs the
+  //   epilogue on every group and leaves the counter at zero.
   int* published = p.counters + tt;
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(p.part, 0, p.part_bytes, kBufferRsrcWord3);
   auto off = [&](int qq, int mat, int g, int v4) {  // byte offset of this lane's chunk in piece qq's slot
     return (uint32_t)(tt * ks + qq) * PART_BYTES + (uint32_t)((((wave * NM + mat) * MG + g) * 4 + v4) * 64 + lane) * 16u;
   };
-  if (q < ks - 1) {
+  if (dist || q < ks - 1) {
 #pragma unroll
     for (int mat = 0; mat < NM; ++mat)
 #pragma unroll
-      for (int g = 0; g < MG; ++g)
+      for (int g = 0; g < MG; ++g) {
+        if (dist && ((gmask >> g) & 1u)) continue;
 #pragma unroll
         for (int v4 = 0; v4 < 4; ++v4) store_coherent(prs, off(q, mat, g, v4), own(mat, g, v4));
+      }
     wait_stores();
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_fetch_add(published, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
+    if (!dist) return;
   }
   rload();
   if (threadIdx.x == 0) {
-    while (__hip_atomic_load(published, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < ks - 1)
+    const int need = dist ? ks : ks - 1;
+    while (__hip_atomic_load(published, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need)
       __builtin_amdgcn_s_sleep(2);
-    __hip_atomic_store(published, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!dist)
+      __hip_atomic_store(published, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else if (__hip_atomic_fetch_add(published, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 2 * ks - 1)
+      __hip_atomic_store(published, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  auto fold = [&](auto ksc) {  // every chunk's ks - 1 loads issued unconditionally
+  // the other pieces in K order: piece r + (r >= q) for r < ks - 1 (this piece is ks - 1 unless
+  // dist), every chunk's ks - 1 loads issued unconditionally
+  const int skip = dist ? q : ks - 1;
+  auto fold = [&](auto ksc) {
     constexpr int KS = decltype(ksc)::value;
     epilogue([&](int mat, int g, int v4) {
       f32x4 v[KS - 1];
 #pragma unroll
-      for (int r = 0; r < KS - 1; ++r) v[r] = load_coherent(prs, off(r, mat, g, v4));
+      for (int r = 0; r < KS - 1; ++r) v[r] = load_coherent(prs, off(r + (r >= skip ? 1 : 0), mat, g, v4));
       f32x4 sum = v[0];
 #pragma unroll
       for (int r = 1; r < KS - 1; ++r) sum += v[r];
