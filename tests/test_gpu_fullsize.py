@@ -293,11 +293,24 @@ def test_poisoned_outputs_and_guard_bands(pkg, cuda, fmt, M):
     """Every forward entry point with NaN in its output and in every workspace byte past the
     arrival counters: the results are finite and pass the bar, nothing is written outside the
     output and the workspace, and the inputs are unchanged."""
+    _poisoned_case(pkg, cuda, fmt, M, 1024, 3072)
+
+
+@pytest.mark.parametrize("fmt", ["bfp8", "bf4"])
+@pytest.mark.parametrize("H,I", [(1024, 4352), (5376, 2048)])
+def test_poisoned_split_pieces(pkg, cuda, fmt, H, I):
+    """The poisoned-buffer checks at 2048 tokens on shapes whose last tiles split their K range
+    (gate/up at I = 4352: 16 tiles in 4 pieces; down at H = 5376: 80 tiles in 3 pieces), so that
+    the pieces' partial tiles go through the NaN-filled workspace and their counters must come
+    back to zero."""
+    _poisoned_case(pkg, cuda, fmt, 2048, H, I)
+
+
+def _poisoned_case(pkg, cuda, fmt, M, H, I):
     import torch
     from qwen_mlp_amd import _lib, workloads
 
-    H, I = 1024, 3072
-    print(f"case poisoned {fmt} M={M}", flush=True)
+    print(f"case poisoned {fmt} H={H} I={I} M={M}", flush=True)
     sd = workloads.state_dict(H, I, layer=40, device=cuda)
     w = pkg.load_mlp_weights(cuda, sd, weight_format=fmt)
     hw = host_weights(pkg, sd, fmt)
