@@ -47,6 +47,7 @@ struct TlParams {
   int ks;                // down projection: K splits per tile of the K-split part (1: no split)
   int nfull;             // leading blocks that cover whole K ranges of feature blocks 0, 1, ...
                          // (tiled_kernel; the K-split part follows them in the same launch)
+  int ntail;             // tiled32_kernel: split tiles (blocks of padding tiles beyond exit)
   float* part;           // ks > 1: fp32 partial tiles, [tile][K split][block's outputs]
   int part_bytes;
   int* counters;         // ks > 1: arrival counter per tile (tiled_kernel), publication counter
@@ -417,7 +418,9 @@ struct Tl32Stage {
   typename StepWord<WF>::type w[NM][WF ? 2 : 4];
 };
 
-constexpr int kSplitMaxPieces = 4;  // K pieces per split tile of tiled32_kernel
+// K pieces per split tile of tiled32_kernel: 4 for the gate/up pair, 8 for the down projection
+// (the last sums request every piece's chunks of a token group at once)
+constexpr int kSplitMaxPieces = 8;
 
 // NM = 2: gate/up (the wave's 32-row feature pair of both matrices); NM = 1: the down projection
 // (one 32-row unit of its matrix per wave, residual epilogue).
@@ -452,18 +455,20 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   const int P = full ? p.nfull : (int)gridDim.x - p.nfull;
   const int L = full || (P / 8) % ks == 0 ? xcd_logical(b, P) : b;
   const int tt = L / ks, q = L % ks;  // split tiles: index among them, piece
+  if (!full && tt >= p.ntail) return;  // a padding tile (the split tiles rounded up to whole XCDs)
   const int tile = full ? L : p.nfull + tt;
   const int bn = p.bn0 + tile / p.nbm, bm = tile % p.nbm;
   const int m0 = bm * MG * 32;
   const int pair = bn * NWV + wave;  // the wave's 32-row unit (of each matrix)
   const int k0 = q * p.C / ks, nsb = (q + 1) * p.C / ks - k0;  // the piece's superblocks
   // A split tile whose pieces share an XCD (consecutive in its dispatch order) is finished by all
-  // of them, each the token groups g with g % ks == q (gmask); otherwise by its last piece.
-  const bool dist = !full && P % 8 == 0 && (P / 8) % ks == 0 && ks <= MG;
+  // of them: piece q the (wave, token group) units u = wave * MG + g with u % ks == q (gmask:
+  // this wave's groups); otherwise by its last piece.
+  const bool dist = !full && P % 8 == 0 && (P / 8) % ks == 0 && ks <= NWV * MG;
   uint32_t gmask = 0;
 #pragma unroll
   for (int g = 0; g < MG; ++g)
-    if (ks == 1 || !dist || g % ks == q) gmask |= 1u << g;
+    if (ks == 1 || !dist || (wave * MG + g) % ks == q) gmask |= 1u << g;
   const int kb = k0 * kSteps, nst = nsb * kSteps;
 
   // The epilogue's exponents (the block's NM x 256 row exponents, its 128 tokens' exponents)
@@ -844,13 +849,23 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
       return sum + own(mat, g, v4);
     });
   };
-  static_assert(kSplitMaxPieces == 4, "fold instances");
+  static_assert(kSplitMaxPieces == 8, "fold instances");
   if (ks == 2)
     fold(std::integral_constant<int, 2>{});
   else if (ks == 3)
     fold(std::integral_constant<int, 3>{});
-  else
+  else if (ks == 4 || NM == 2)  // the gate/up pair splits 4 ways at most
     fold(std::integral_constant<int, 4>{});
+  else if constexpr (NM == 1) {
+    if (ks == 5)
+      fold(std::integral_constant<int, 5>{});
+    else if (ks == 6)
+      fold(std::integral_constant<int, 6>{});
+    else if (ks == 7)
+      fold(std::integral_constant<int, 7>{});
+    else
+      fold(std::integral_constant<int, 8>{});
+  }
 }
 
 // ---------------------------------------------------------------- host side
@@ -954,34 +969,36 @@ constexpr size_t split_part_bytes(int NM, int MG) { return (size_t)kTlNWV * NM *
 
 // Whole rounds plus K-split pieces for a tiled32 projection of ntiles tiles of C superblocks on
 // `slots` resident blocks: the first rounds x slots tiles run whole; the remaining ntail tiles
-// split K into ks <= kSplitMaxPieces pieces with ntail x ks <= slots, so that the pieces fill at
-// most one more round.  ks = 1 (no split) where there is no whole round or no remainder, where
-// fewer than two pieces per tile fit, or where the workspace region does not hold the pieces'
-// partial tiles.
+// split K into ks <= 4 pieces with ntail x ks <= slots, so that the pieces fill at most one more
+// round.  With fewer tiles than slots (a few dozen to a few hundred tokens) every tile splits, up
+// to max_ks ways, its tiles rounded up to a multiple of 8 (whole XCDs; the padding blocks exit at
+// once) so that each tile's pieces share an XCD.  ks = 1 (no split) where there is no remainder,
+// where fewer than two pieces per tile fit, or where the workspace region does not hold the
+// pieces' partial tiles.
 struct SplitPlan {
   int nfull, ntail, ks;
+  int npad;  // split tiles including the padding: the launch has nfull + npad x ks blocks
 };
-static SplitPlan split_plan(int ntiles, int C, int slots, size_t part_bytes, size_t piece_bytes) {
-  const SplitPlan none{ntiles, 0, 1};
+static SplitPlan split_plan(int ntiles, int C, int slots, size_t part_bytes, size_t piece_bytes, int max_ks) {
+  const SplitPlan none{ntiles, 0, 1, 0};
   if (slots < 1) return none;
   const int rounds = ntiles / slots, ntail = ntiles - rounds * slots;
-  if (rounds == 0 || ntail == 0 || 2 * (long long)ntail > kMaxDim / kTileRows) return none;
-  int ks = std::min(std::min(slots / ntail, C), kSplitMaxPieces);
+  if (ntail == 0 || 2 * (long long)ntail > kMaxDim / kTileRows) return none;
+  const int npad = rounds ? ntail : (ntail + 7) / 8 * 8;
+  int ks = std::min(std::min(slots / npad, C), rounds ? 4 : max_ks);
   while (ks > 1 && (size_t)ntail * ks * piece_bytes > part_bytes) --ks;
   if (ks < 2) return none;
-  return {rounds * slots, ntail, ks};
+  return {rounds * slots, ntail, ks, npad};
 }
 
 // Sized for the most any split can hold on kSplitMaxSlots resident blocks (one per CU of a 256-CU
-// device), as soon as either projection has more tiles than that (the first M that can split):
-// constant beyond, so that the workspace never shrinks as M grows (the plan's own need does:
-// 64 tail tiles at 2048 tokens, none at 2049).  split_plan checks the size against the device's
-// own block count at launch.
+// device) at every M that takes the many-token kernels: constant in M, so that the workspace never
+// shrinks as M grows (the plan's own need does: 64 tail tiles at 2048 tokens, none at 2049).
+// split_plan checks the size against the device's own block count at launch.
 size_t tiled_split_bytes(int M, int H, int I, int fmt) {
+  (void)H;
+  (void)I;
   if (fmt == 0 || M <= 32) return 0;  // bf16 weights, or no many-token kernels
-  const long long nbm = (M + kTl32MG * 32 - 1) / (kTl32MG * 32), tile_features = kTlNWV * 2 * kTileRows;
-  const long long tiles = std::max(I / tile_features, H / tile_features) * nbm;
-  if (tiles <= kSplitMaxSlots) return 0;
   return (size_t)kSplitMaxSlots * std::max(split_part_bytes(2, kTl32MG), split_part_bytes(1, kTl32MG));
 }
 
@@ -994,9 +1011,10 @@ static int launch_tiled32_plan(TlParams p, int bn0, int nbm, const SplitPlan& sp
   p.nbm = nbm;
   p.bn0 = bn0;
   p.nfull = sp.nfull;
+  p.ntail = sp.ntail;
   p.ks = sp.ks;
   const size_t lds = tiled32_lds(MG, NM);
-  launch_timed_part(slot, marks, tiled32_kernel<WF, MG, NBB, NM>, dim3(sp.nfull + sp.ntail * sp.ks),
+  launch_timed_part(slot, marks, tiled32_kernel<WF, MG, NBB, NM>, dim3(sp.nfull + sp.npad * sp.ks),
                     dim3(kTlNWV * 64), lds, s, p);
   return check_launch("tiled32_kernel");
 }
@@ -1009,27 +1027,30 @@ static int launch_tiled32(TlParams p, int num_cus, hipStream_t s) {
   const int nbm = (p.M + MG * 32 - 1) / (MG * 32);
   const int slots = num_cus * blocks_per_cu((const void*)tiled32_kernel<WF, MG, NBB, 2>, tiled32_lds(MG, 2));
   const SplitPlan sp =
-      p.part ? split_plan(nbn * nbm, p.C, slots, (size_t)p.part_bytes, split_part_bytes(2, MG)) : SplitPlan{0, 0, 1};
+      p.part ? split_plan(nbn * nbm, p.C, slots, (size_t)p.part_bytes, split_part_bytes(2, MG), 4)
+             : SplitPlan{0, 0, 1, 0};
   if (sp.ks > 1) return launch_tiled32_plan<WF, MG, NBB, 2>(p, 0, nbm, sp, 0, 3, s);
   const int main = tail_split(nbn, nbm, slots);
-  if (main == nbn || main == 0) return launch_tiled32_plan<WF, MG, NBB, 2>(p, 0, nbm, {nbn * nbm, 0, 1}, 0, 3, s);
-  if (int rc = launch_tiled32_plan<WF, MG, NBB, 2>(p, 0, nbm, {main * nbm, 0, 1}, 0, 1, s)) return rc;
+  if (main == nbn || main == 0)
+    return launch_tiled32_plan<WF, MG, NBB, 2>(p, 0, nbm, {nbn * nbm, 0, 1, 0}, 0, 3, s);
+  if (int rc = launch_tiled32_plan<WF, MG, NBB, 2>(p, 0, nbm, {main * nbm, 0, 1, 0}, 0, 1, s)) return rc;
   const int nbm1 = (p.M + 31) / 32;
-  return launch_tiled32_plan<WF, 1, NBB, 2>(p, main, nbm1, {(nbn - main) * nbm1, 0, 1}, 0, 2, s);
+  return launch_tiled32_plan<WF, 1, NBB, 2>(p, main, nbm1, {(nbn - main) * nbm1, 0, 1, 0}, 0, 2, s);
 }
 
 // bfp8 down projection on tiled32_kernel (NM = 1): each wave owns one 32-row unit x 4 groups of 32
 // tokens, a block 256 features x 128 tokens, as whole rounds plus K-split pieces.  Returns 1
 // (nothing launched) where that plan has no whole round or no split: then tiled_kernel runs the
 // projection.
+template <int MG>
 static int launch_down32(TlParams p, int num_cus, hipStream_t s) {
-  constexpr int MG = kTl32MG, NBB = 3;
+  constexpr int NBB = 3;
   if (p.N % (kTlNWV * 2 * kTileRows)) return 1;
   const int nbn = p.N / (kTlNWV * 2 * kTileRows), nbm = (p.M + MG * 32 - 1) / (MG * 32);
   const int slots = num_cus * blocks_per_cu((const void*)tiled32_kernel<1, MG, NBB, 1>, tiled32_lds(MG, 1));
   const int ntiles = nbn * nbm;
-  SplitPlan sp = p.part ? split_plan(ntiles, p.C, slots, (size_t)p.part_bytes, split_part_bytes(1, MG))
-                        : SplitPlan{ntiles, 0, 1};
+  SplitPlan sp = p.part ? split_plan(ntiles, p.C, slots, (size_t)p.part_bytes, split_part_bytes(1, MG), 8)
+                        : SplitPlan{ntiles, 0, 1, 0};
   if (sp.ks == 1 && !(ntiles >= slots && ntiles % slots == 0)) return 1;
   return launch_tiled32_plan<1, MG, NBB, 1>(p, 0, nbm, sp, 1, 3, s);
 }
@@ -1069,8 +1090,10 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.part_bytes = (int)std::min<size_t>(L.split_bytes, (size_t)1 << 30);
   g.counters = (int*)(a.ws + L.counters_gu);
   constexpr int GT = kTlGuTPW, GM = kTlGuMG, DT = kTlDnTPW, DM = kTlDnMG;
-  int rc = fmt == 2   ? launch_tiled32<2, kTl32MG, 3>(g, num_cus, s)
-           : fmt == 1 ? launch_tiled32<1, kTl32MG, 2>(g, num_cus, s)
+  // block-float: tiles of 2 groups of 32 tokens up to 64 tokens, of 4 beyond
+  const bool narrow = a.M <= 2 * 32;
+  int rc = fmt == 2   ? (narrow ? launch_tiled32<2, 2, 3>(g, num_cus, s) : launch_tiled32<2, kTl32MG, 3>(g, num_cus, s))
+           : fmt == 1 ? (narrow ? launch_tiled32<1, 2, 2>(g, num_cus, s) : launch_tiled32<1, kTl32MG, 2>(g, num_cus, s))
                       : launch_tiled<0, 2, GT, GM, 2, GM / 4>(g, num_cus, s);
   if (rc) return rc;
   TlParams d{};
@@ -1096,7 +1119,7 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
     d32.part = L.split_bytes ? (float*)(a.ws + L.split) : nullptr;
     d32.part_bytes = (int)std::min<size_t>(L.split_bytes, (size_t)1 << 30);
     d32.counters = (int*)(a.ws + L.counters_d);
-    rc = launch_down32(d32, num_cus, s);
+    rc = narrow ? launch_down32<2>(d32, num_cus, s) : launch_down32<kTl32MG>(d32, num_cus, s);
     if (rc != 1) return rc;
   }
   rc = dfmt == 1 ? launch_tiled<1, 1, DT, DM, 3, DM>(d, num_cus, s) : launch_tiled<0, 1, DT, DM, 3, DM>(d, num_cus, s);

@@ -88,6 +88,31 @@ def test_rmsnorm_prologue_27b_m2048_sampled_rows(pkg, cuda):
     check(y.cpu().numpy()[rows], ref, f"rmsnorm prefill 27B M={M} bfp8 ({len(rows)} sampled rows)")
 
 
+@pytest.mark.parametrize("fmt", ["bfp8", "bf4"])
+@pytest.mark.parametrize("M", [48, 64, 128, 256])
+def test_midwidth_27b_sampled_rows(pkg, cuda, fmt, M):
+    """The 27B layer at a few dozen to a few hundred tokens (long verify windows, short prefill
+    chunks): fewer tiles than CUs, so every tile splits its K range (gate/up 3-4 pieces, down up to
+    8) and the pieces finish the tile together; checked on the sampled rows of every 64-token
+    block, the bf16 output against the fp32 one rounded once."""
+    import torch
+    from qwen_mlp_amd import workloads
+
+    print(f"case midwidth 27B M={M} {fmt}", flush=True)
+    sd = workloads.state_dict(H27, I27, layer=12, device=cuda)
+    w = pkg.load_mlp_weights(cuda, sd, weight_format=fmt)
+    x = workloads.activations(M, H27, seed=4300 + M, device=cuda)
+    ws = pkg.new_workspace(M, H27, I27, fmt, cuda)
+    y32 = pkg.mlp_forward(x, w, residual=x, workspace=ws, out_dtype=torch.float32)
+    y16 = pkg.mlp_forward(x, w, residual=x, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y32.to(torch.bfloat16), y16), "bf16 output is not the fp32 output rounded once"
+    rows = _sample_rows(M)
+    hw = host_weights(pkg, sd, fmt)
+    ref = oracle(x.float().cpu().numpy()[rows], hw)
+    check(y32.cpu().numpy()[rows], ref, f"midwidth 27B M={M} {fmt} ({len(rows)} sampled rows)")
+
+
 # ---------------------------------------------------------------- 64-layer stack
 
 
