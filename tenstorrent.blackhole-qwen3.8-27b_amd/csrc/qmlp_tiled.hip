@@ -460,7 +460,12 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   const int bn = p.bn0 + tile / p.nbm, bm = tile % p.nbm;
   const int m0 = bm * MG * 32;
   const int pair = bn * NWV + wave;  // the wave's 32-row unit (of each matrix)
-  const int k0 = q * p.C / ks, nsb = (q + 1) * p.C / ks - k0;  // the piece's superblocks
+  // The piece's 64-K steps [kb, kb + nst) (every step of the K range for a whole tile; pieces cut
+  // at step granularity, so that they differ by one step at most) and the superblocks they touch,
+  // [k0, k0 + nsb); ph: the first step's position inside its superblock.
+  const int kst = p.C * kSteps;
+  const int kb = q * kst / ks, nst = (q + 1) * kst / ks - kb;
+  const int k0 = kb / kSteps, nsb = (kb + nst - 1) / kSteps - k0 + 1, ph = kb % kSteps;
   // A split tile whose pieces share an XCD (consecutive in its dispatch order) is finished by all
   // of them: piece q the (wave, token group) units u = wave * MG + g with u % ks == q (gmask:
   // this wave's groups); otherwise by its last piece.
@@ -469,7 +474,6 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
 #pragma unroll
   for (int g = 0; g < MG; ++g)
     if (ks == 1 || !dist || (wave * MG + g) % ks == q) gmask |= 1u << g;
-  const int kb = k0 * kSteps, nst = nsb * kSteps;
 
   // The epilogue's exponents (the block's NM x 256 row exponents, its 128 tokens' exponents)
   // staged in LDS after the B ring: requested first, written to LDS before the first barrier, read
@@ -688,11 +692,11 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     run_steps<U>(s, nst, [&](int k, int s) {
       Tl32Stage<WF, NM>& cur = stage(k % 3);
       u32x4(&bw)[CPT] = k % 3 == 0 ? b2 : (k % 3 == 1 ? b0 : b1);
-      compute(cur, s, s & 3);
+      compute(cur, s, (s + ph) & 3);
       wload(cur, s + 3);
       bstore(bw, s + 2);
       bload(bw, s + 5);
-      if ((s & 3) == 3) erotate(s / kSteps);
+      if (((s + ph) & 3) == 3) erotate((s + ph) / kSteps);
       __syncthreads();
     });
   } else {
@@ -702,13 +706,13 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
       u32x4(&bnext)[CPT] = k % 2 == 0 ? b1 : b2;
       u32x4(&bwrite)[CPT] = k % 2 == 0 ? b2 : b1;
       bload(bnext, s + 3);
-      compute(cur, s, s & 3);
+      compute(cur, s, (s + ph) & 3);
       // keeps the next weight loads behind the products: hoisted above them, their registers
       // make the compiler wait for every LDS read before its two products
       __builtin_amdgcn_sched_barrier(0);
       wload(cur, s + 3);
       bstore(bwrite, s + 2);
-      if ((s & 3) == 3) erotate(s / kSteps);
+      if (((s + ph) & 3) == 3) erotate((s + ph) / kSteps);
       __syncthreads();
     });
   }
