@@ -1094,8 +1094,12 @@ int launch_forward_tiled(const ForwardArgs& a, int num_cus, hipStream_t s) {
   g.part_bytes = (int)std::min<size_t>(L.split_bytes, (size_t)1 << 30);
   g.counters = (int*)(a.ws + L.counters_gu);
   constexpr int GT = kTlGuTPW, GM = kTlGuMG, DT = kTlDnTPW, DM = kTlDnMG;
-  // block-float: tiles of 2 groups of 32 tokens up to 64 tokens, of 4 beyond
-  const bool narrow = a.M <= 2 * 32;
+  // block-float: tiles of 2 groups of 32 tokens where that pads fewer token columns than tiles
+  // of 4 (at most 256 tokens: up to 64 and from 129 to 192), of 4 otherwise.  Measured at the 27B
+  // shape: 2 groups 111-113 against 269-275 us (the 4-group tiles before every tile split) at
+  // 33-64 tokens, 162-166 against 194-196 us at 160-192; 4 groups 133 against 145 us at 96-128
+  // and level at 224-256.
+  const bool narrow = a.M <= 256 && (a.M + 63) / 64 * 64 < (a.M + 127) / 128 * 128;
   int rc = fmt == 2   ? (narrow ? launch_tiled32<2, 2, 3>(g, num_cus, s) : launch_tiled32<2, kTl32MG, 3>(g, num_cus, s))
            : fmt == 1 ? (narrow ? launch_tiled32<1, 2, 2>(g, num_cus, s) : launch_tiled32<1, kTl32MG, 2>(g, num_cus, s))
                       : launch_tiled<0, 2, GT, GM, 2, GM / 4>(g, num_cus, s);

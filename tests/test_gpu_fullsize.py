@@ -89,7 +89,7 @@ def test_rmsnorm_prologue_27b_m2048_sampled_rows(pkg, cuda):
 
 
 @pytest.mark.parametrize("fmt", ["bfp8", "bf4"])
-@pytest.mark.parametrize("M", [48, 64, 128, 256])
+@pytest.mark.parametrize("M", [48, 64, 128, 160, 256])
 def test_midwidth_27b_sampled_rows(pkg, cuda, fmt, M):
     """The 27B layer at a few dozen to a few hundred tokens (long verify windows, short prefill
     chunks): fewer tiles than CUs, so every tile splits its K range (gate/up 3-4 pieces, down up to
