@@ -88,8 +88,8 @@ WsLayout ws_layout(int M, int H, int I, int fmt) {
   L.x16 = off;
   off = align256(off + (fmt != QMLP_FMT_BF16 ? (size_t)M * H * 2 : 0));
   L.xn = off;  // bf16 [M, H]: the normalised activations when the RMSNorm runs as its own pass
-  // The partial tiles of the many-token 32x32 kernels' K-split pieces (block-float formats) share
-  // xn's place: xn is read only by the activation prep, before either projection.
+  // The partial tiles of the many-token kernels' K-split pieces share xn's place: xn is read only
+  // before the gate/up projection (by the activation prep, or by gate/up itself for bf16 weights).
   L.split = off;
   L.split_bytes = tiled_split_bytes(M, H, I, fmt);
   off = align256(off + std::max((size_t)M * H * 2, L.split_bytes));

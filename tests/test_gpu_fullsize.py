@@ -88,13 +88,14 @@ def test_rmsnorm_prologue_27b_m2048_sampled_rows(pkg, cuda):
     check(y.cpu().numpy()[rows], ref, f"rmsnorm prefill 27B M={M} bfp8 ({len(rows)} sampled rows)")
 
 
-@pytest.mark.parametrize("fmt", ["bfp8", "bf4"])
+@pytest.mark.parametrize("fmt", ["bfp8", "bf4", "bf16"])
 @pytest.mark.parametrize("M", [48, 64, 128, 160, 256])
 def test_midwidth_27b_sampled_rows(pkg, cuda, fmt, M):
     """The 27B layer at a few dozen to a few hundred tokens (long verify windows, short prefill
     chunks): fewer tiles than CUs, so every tile splits its K range (gate/up 3-4 pieces, down up to
-    8) and the pieces finish the tile together; checked on the sampled rows of every 64-token
-    block, the bf16 output against the fp32 one rounded once."""
+    8; with bf16 weights the down projection only) and the pieces finish the tile together;
+    checked on the sampled rows of every 64-token block, the bf16 output against the fp32 one
+    rounded once."""
     import torch
     from qwen_mlp_amd import workloads
 
