@@ -318,7 +318,7 @@ def main():
             # width sweep
             sweep = {}
             lq = make_layers(pkg, workloads, wl, args.rotate, dev)
-            for M in (1, 32):
+            for M in (1, 32, 64, 256):  # 64 / 256: the many-token kernels with every tile split
                 xm = workloads.activations(M, wl.hidden, gain=wl.gain, device=dev)
                 msm, _ = time_layers(pkg, lq, xm, max(50, args.steps // 2), 10)
                 b = wl.weight_bytes() + 4 * M * wl.hidden
