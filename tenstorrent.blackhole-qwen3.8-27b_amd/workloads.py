@@ -47,6 +47,8 @@ WORKLOADS = {
     "qwen3-27b-mlp-m16-bfp8": Workload("qwen3-27b-mlp-m16-bfp8", 5120, 17408, 16, "bfp8", True),
     "qwen3-27b-mlp-m1-bfp8": Workload("qwen3-27b-mlp-m1-bfp8", 5120, 17408, 1, "bfp8", True),
     "qwen3-27b-mlp-m32-bfp8": Workload("qwen3-27b-mlp-m32-bfp8", 5120, 17408, 32, "bfp8", True),
+    # a 64-token verify window: the many-token kernels with every tile split
+    "qwen3-27b-mlp-m64-bfp8": Workload("qwen3-27b-mlp-m64-bfp8", 5120, 17408, 64, "bfp8", True),
     "qwen3-27b-mlp-prefill-m2048-bfp8": Workload("qwen3-27b-mlp-prefill-m2048-bfp8", 5120, 17408, 2048, "bfp8", False),
     "qwen3-27b-mlp-m16-bf4": Workload("qwen3-27b-mlp-m16-bf4", 5120, 17408, 16, "bf4", True),
     "qwen3-27b-mlp-m1-bf4": Workload("qwen3-27b-mlp-m1-bf4", 5120, 17408, 1, "bf4", True),

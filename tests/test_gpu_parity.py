@@ -133,7 +133,7 @@ def test_pack_reports_flushed_groups(pkg, cuda):
 @pytest.mark.parametrize("name", ["plumbing-h1024-i3072-m1-bf16", "qwen3-27b-mlp-m16-bf16", "qwen3-27b-mlp-m16-bfp8",
                                   "qwen3-27b-mlp-m1-bfp8", "qwen3-27b-mlp-m32-bfp8", "qwen3-27b-mlp-m16-bf4",
                                   "qwen3-27b-mlp-m1-bf4", "qwen3-27b-mlp-m32-bf4", "qwen3-27b-tp2-share-m16-bfp8",
-                                  "qwen3-27b-tp2-share-m16-bf4"])
+                                  "qwen3-27b-tp2-share-m16-bf4", "qwen3-27b-mlp-m64-bfp8"])
 def test_forward_workloads(pkg, cuda, name):
     import torch
     from qwen_mlp_amd import workloads
