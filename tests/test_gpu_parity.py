@@ -290,16 +290,16 @@ def test_bitwise_deterministic(pkg, cuda, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
-@pytest.mark.parametrize("H,I", [(1024, 4352), (5376, 2048)])
-def test_prefill_bitwise_deterministic(pkg, cuda, fmt, H, I):
-    """2048-token forwards repeated give identical bits, also where the last tiles split their K
-    range into pieces whose partial tiles meet in the workspace (gate/up at I = 4352: 16 tiles in
-    4 pieces; down at H = 5376: 80 tiles in 3 pieces) and are added in a fixed order."""
+@pytest.mark.parametrize("H,I,M", [(1024, 4352, 2048), (5376, 2048, 2048), (1024, 3072, 64)])
+def test_prefill_bitwise_deterministic(pkg, cuda, fmt, H, I, M):
+    """Many-token forwards repeated give identical bits, also where tiles split their K range into
+    pieces whose partial tiles meet in the workspace and are added in a fixed order: at 2048
+    tokens the tiles beyond the last whole round (gate/up at I = 4352: 16 tiles in 4 pieces; down
+    at H = 5376: 80 tiles in 3 pieces), at 64 tokens every tile."""
     import torch
     from qwen_mlp_amd import workloads
 
-    M = 2048
-    print(f"case prefill determinism {fmt} H={H} I={I}", flush=True)
+    print(f"case prefill determinism {fmt} H={H} I={I} M={M}", flush=True)
     sd = workloads.state_dict(H, I, layer=5, device=cuda)
     mlp = pkg.Qwen36MLP(cuda, sd, weight_format=fmt, max_tokens=M)
     x = workloads.activations(M, H, seed=7391 + M, device=cuda)
@@ -313,12 +313,12 @@ def test_prefill_bitwise_deterministic(pkg, cuda, fmt, H, I):
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "bfp8", "bf4"])
-@pytest.mark.parametrize("H,I,M", [(1024, 3072, 16), (1024, 4352, 2048)])
+@pytest.mark.parametrize("H,I,M", [(1024, 3072, 16), (1024, 3072, 64), (1024, 4352, 2048)])
 def test_graph_capture_replays(pkg, cuda, fmt, H, I, M):
     """A forward captured in a HIP graph and replayed five times on new inputs, each replay
-    equal to the eager forward: the weight-streaming kernels at 16 tokens and the tiled kernels
-    at 2048 tokens with split pieces (their arrival counters must be back at zero after every
-    replay)."""
+    equal to the eager forward: the weight-streaming kernels at 16 tokens, the tiled kernels at 64
+    tokens (every tile split, padding blocks) and at 2048 tokens with split pieces (their arrival
+    counters must be back at zero after every replay)."""
     import torch
     from qwen_mlp_amd import workloads
 
