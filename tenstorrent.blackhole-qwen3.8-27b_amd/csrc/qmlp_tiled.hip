@@ -426,14 +426,15 @@ constexpr int kSplitMaxPieces = 8;
 // (one 32-row unit of its matrix per wave, residual epilogue).
 //
 // Work: blocks [0, nfull) each take one whole tile (tile = the block's logical index, feature
-// blocks from bn0); blocks from nfull take K pieces of the tiles that follow: ks consecutive
-// blocks share a tile, piece q covering superblocks [q C / ks, (q + 1) C / ks).  The whole tiles
+// blocks from bn0); blocks from nfull take K pieces of the ntail tiles that follow (rounded up to
+// whole XCDs where every tile splits: the padding blocks exit at once): ks consecutive blocks
+// share a tile, piece q covering 64-K steps [q S / ks, (q + 1) S / ks) of its S.  The whole tiles
 // come in complete rounds of resident blocks and the pieces start together as those rounds end,
 // so the blocks reading one feature block's weights read the same K range at the same time (L2
 // reuse).  A split tile's pieces meet through the workspace: where they share an XCD each piece
-// finishes a share of the tile's token groups (it publishes the others' groups, then adds the
-// other pieces' partials of its own); elsewhere pieces 0 .. ks-2 publish their partial tiles and
-// piece ks-1 adds them in K order and runs the epilogue.
+// finishes a share of the tile's (wave, token group) units (it publishes the others' units, then
+// adds the other pieces' partials of its own); elsewhere pieces 0 .. ks-2 publish their partial
+// tiles and piece ks-1 adds them in K order and runs the epilogue.
 template <int WF, int MG, int NBB, int NM>
 __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   constexpr int NWV = 8, NT = NWV * 64;
@@ -796,13 +797,13 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     return;
   }
 
-  // Split tile.  Every piece publishes, in its slot (tt, q), the groups it does not finish and
-  // counts itself published.
+  // Split tile.  Every piece publishes, in its slot (tt, q), the units it does not finish (all of
+  // them unless dist) and counts itself published.
   // * dist (the pieces share an XCD and are consecutive in its dispatch order, so all of them
   //   become resident: the XCD dispatches in order and holds more blocks than a tile has
   //   pieces): each piece waits for all ks publications, adds the other pieces' partials of its
-  //   own groups in K order and its own last (deterministic per group), and runs the epilogue on
-  //   those groups.  Each piece counts itself once more after its wait; the last of those
+  //   own units in K order and its own last (deterministic per unit), and runs the epilogue on
+  //   those units.  Each piece counts itself once more after its wait; the last of those
   //   leaves the counter at zero.
   // * otherwise piece ks-1, the tile's last block in dispatch order (the others are resident or
   //   done when it runs, so its wait cannot be held up), waits for the ks-1 publications of the
