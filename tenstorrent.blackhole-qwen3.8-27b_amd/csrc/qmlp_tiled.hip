@@ -431,10 +431,10 @@ constexpr int kSplitMaxPieces = 8;
 // share a tile, piece q covering 64-K steps [q S / ks, (q + 1) S / ks) of its S.  The whole tiles
 // come in complete rounds of resident blocks and the pieces start together as those rounds end,
 // so the blocks reading one feature block's weights read the same K range at the same time (L2
-// reuse).  A split tile's pieces meet through the workspace: where they share an XCD each piece
-// finishes a share of the tile's (wave, token group) units (it publishes the others' units, then
-// adds the other pieces' partials of its own); elsewhere pieces 0 .. ks-2 publish their partial
-// tiles and piece ks-1 adds them in K order and runs the epilogue.
+// reuse).  A split tile's pieces meet through the workspace by last arrival: every piece
+// publishes its partial tile and counts itself, and the last to count adds the ks partials in K
+// order and runs the epilogue.  No block ever waits for another, so the kernel cannot stall
+// whatever else holds the CUs (other streams, other processes).
 template <int WF, int MG, int NBB, int NM>
 __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   constexpr int NWV = 8, NT = NWV * 64;
@@ -450,9 +450,8 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   const bool full = (int)blockIdx.x < p.nfull;
   const int b = full ? (int)blockIdx.x : (int)blockIdx.x - p.nfull;
   const int ks = full ? 1 : p.ks;
-  // blocks sharing weights share an XCD; the pieces of a split tile keep their order (piece
-  // ks - 1 has the highest block index of its tile), which needs ks to divide the part's blocks
-  // per XCD
+  // blocks sharing weights share an XCD (the pieces of a split tile too, where ks divides the
+  // part's blocks per XCD: their partial tiles then meet in one L2)
   const int P = full ? p.nfull : (int)gridDim.x - p.nfull;
   const int L = full || (P / 8) % ks == 0 ? xcd_logical(b, P) : b;
   const int tt = L / ks, q = L % ks;  // split tiles: index among them, piece
@@ -467,15 +466,6 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   const int kst = p.C * kSteps;
   const int kb = q * kst / ks, nst = (q + 1) * kst / ks - kb;
   const int k0 = kb / kSteps, nsb = (kb + nst - 1) / kSteps - k0 + 1, ph = kb % kSteps;
-  // A split tile whose pieces share an XCD (consecutive in its dispatch order) is finished by all
-  // of them: piece q the (wave, token group) units u = wave * MG + g with u % ks == q (gmask:
-  // this wave's groups); otherwise by its last piece.
-  const bool dist = !full && P % 8 == 0 && (P / 8) % ks == 0 && ks <= NWV * MG;
-  uint32_t gmask = 0;
-#pragma unroll
-  for (int g = 0; g < MG; ++g)
-    if (ks == 1 || !dist || (wave * MG + g) % ks == q) gmask |= 1u << g;
-
   // The epilogue's exponents (the block's NM x 256 row exponents, its 128 tokens' exponents)
   // staged in LDS after the B ring: requested first, written to LDS before the first barrier, read
   // after the last.  Kept out of the epilogue's global loads, which could not pass its stores.
@@ -516,10 +506,10 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
   const bool loader = NLD == NT || (int)threadIdx.x < NLD;  // whole waves
 
   // Down projection: the residual words of the lane's outputs (group g, rows 8 vq + 0..3 of its
-  // 4-row quarter), requested together after the K loop (by the last piece of a split tile
-  // before its wait), so that they cost one round trip and none of the epilogue's loads waits
-  // behind its stores.  Requested before the loop instead, their completion held up the loop's
-  // first in-order waits (+5 us per block).  bf16: the low two words; fp32: all four.
+  // 4-row quarter), requested together after the K loop (by a split tile's last arrival, with
+  // the other pieces' partials), so that they cost one round trip and none of the epilogue's
+  // loads waits behind its stores.  Requested before the loop instead, their completion held up
+  // the loop's first in-order waits (+5 us per block).  bf16: the low two words; fp32: all four.
   u32x4 rres[NM == 1 ? MG : 1][4];
 #pragma unroll
   for (int g = 0; g < (NM == 1 ? MG : 1); ++g)
@@ -527,11 +517,10 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     for (int vq = 0; vq < 4; ++vq) rres[g][vq] = u32x4{0u, 0u, 0u, 0u};
   auto rload = [&]() {
     if constexpr (NM == 1) {
-      if (!p.residual || (!dist && q != ks - 1)) return;
+      if (!p.residual) return;
       const int col = lane & 31, rq = (lane >> 5) * 4;
 #pragma unroll
       for (int g = 0; g < MG; ++g) {
-        if (!((gmask >> g) & 1u)) continue;
         const size_t row = (size_t)min(m0 + g * 32 + col, p.M - 1) * p.N;
 #pragma unroll
         for (int vq = 0; vq < 4; ++vq) {
@@ -729,7 +718,6 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     const int* ltok = lexp + NM * NWV * 32 + col;  // this lane's token: + 32 g (+ MG * 32: tout)
 #pragma unroll
     for (int g = 0; g < MG; ++g) {
-      if (!((gmask >> g) & 1u)) continue;  // a group another piece of a split tile finishes
       const int m = m0 + g * 32 + col;
       const bool live = m < p.M;
       f32x4 a[NM][4];
@@ -797,61 +785,44 @@ __global__ __launch_bounds__(512) void tiled32_kernel(TlParams p) {
     return;
   }
 
-  // Split tile.  Every piece publishes, in its slot (tt, q), the units it does not finish (all of
-  // them unless dist) and counts itself published.
-  // * dist (the pieces share an XCD and are consecutive in its dispatch order, so all of them
-  //   become resident: the XCD dispatches in order and holds more blocks than a tile has
-  //   pieces): each piece waits for all ks publications, adds the other pieces' partials of its
-  //   own units in K order and its own last (deterministic per unit), and runs the epilogue on
-  //   those units.  Each piece counts itself once more after its wait; the last of those
-  //   leaves the counter at zero.
-  // * otherwise piece ks-1, the tile's last block in dispatch order (the others are resident or
-  //   done when it runs, so its wait cannot be held up), waits for the ks-1 publications of the
-  //   whole partial tiles, adds them in K order, its own last (p_0 + ... + p_{ks-1}), runs the
-  //   epilogue on every group and leaves the counter at zero.
-  int* published = p.counters + tt;
+  // Split tile, finished by last arrival: every piece publishes its whole partial tile in its
+  // slot (tt, q) with write-through stores, waits for them and counts itself; the piece whose
+  // count completes the tile (whichever it is) leaves the counter at zero, reads the ks partial
+  // tiles -- its own among them -- and adds them in K order, p_0 + p_1 + ... + p_{ks-1}, so the
+  // sum does not depend on the arrival order (deterministic), then runs the epilogue on every
+  // group.  No piece waits for another.
+  __shared__ int s_last;
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(p.part, 0, p.part_bytes, kBufferRsrcWord3);
   auto off = [&](int qq, int mat, int g, int v4) {  // byte offset of this lane's chunk in piece qq's slot
     return (uint32_t)(tt * ks + qq) * PART_BYTES + (uint32_t)((((wave * NM + mat) * MG + g) * 4 + v4) * 64 + lane) * 16u;
   };
-  if (dist || q < ks - 1) {
 #pragma unroll
-    for (int mat = 0; mat < NM; ++mat)
+  for (int mat = 0; mat < NM; ++mat)
 #pragma unroll
-      for (int g = 0; g < MG; ++g) {
-        if (dist && ((gmask >> g) & 1u)) continue;
+    for (int g = 0; g < MG; ++g)
 #pragma unroll
-        for (int v4 = 0; v4 < 4; ++v4) store_coherent(prs, off(q, mat, g, v4), own(mat, g, v4));
-      }
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(published, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (!dist) return;
-  }
-  rload();
+      for (int v4 = 0; v4 < 4; ++v4) store_coherent(prs, off(q, mat, g, v4), own(mat, g, v4));
+  wait_stores();
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const int need = dist ? ks : ks - 1;
-    while (__hip_atomic_load(published, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need)
-      __builtin_amdgcn_s_sleep(2);
-    if (!dist)
-      __hip_atomic_store(published, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else if (__hip_atomic_fetch_add(published, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 2 * ks - 1)
-      __hip_atomic_store(published, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int old = __hip_atomic_fetch_add(p.counters + tt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == ks - 1;
+    if (s_last) __hip_atomic_store(p.counters + tt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  // the other pieces in K order: piece r + (r >= q) for r < ks - 1 (this piece is ks - 1 unless
-  // dist), every chunk's ks - 1 loads issued unconditionally
-  const int skip = dist ? q : ks - 1;
+  if (!s_last) return;
+  rload();
+  // every chunk's ks loads issued unconditionally, then added in K order
   auto fold = [&](auto ksc) {
     constexpr int KS = decltype(ksc)::value;
     epilogue([&](int mat, int g, int v4) {
-      f32x4 v[KS - 1];
+      f32x4 v[KS];
 #pragma unroll
-      for (int r = 0; r < KS - 1; ++r) v[r] = load_coherent(prs, off(r + (r >= skip ? 1 : 0), mat, g, v4));
+      for (int r = 0; r < KS; ++r) v[r] = load_coherent(prs, off(r, mat, g, v4));
       f32x4 sum = v[0];
 #pragma unroll
-      for (int r = 1; r < KS - 1; ++r) sum += v[r];
-      return sum + own(mat, g, v4);
+      for (int r = 1; r < KS; ++r) sum += v[r];
+      return sum;
     });
   };
   static_assert(kSplitMaxPieces == 8, "fold instances");
