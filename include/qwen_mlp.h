@@ -51,7 +51,8 @@ typedef struct ihipStream_t* qmlp_stream_t; /* == hipStream_t */
 /* Message for the last failing call on this host thread ("" if none).  Host only. */
 const char* qmlp_last_error(void);
 
-/* Library version string.  Host only. */
+/* Library version string, "qwen_mlp <version> gfx950 src=<digest>": the digest (16 hex digits) is
+ * the sha256 of the kernel sources and this header that the build compiled.  Host only. */
 const char* qmlp_version(void);
 
 /* ---------------------------------------------------------------- weight preparation (load time)
@@ -178,11 +179,13 @@ int qmlp_workspace_init(void* ws, size_t ws_bytes, qmlp_stream_t stream);
  * loops, harnesses that forbid hipMalloc).  The workspace is a QMLP_SCRATCH_BYTES array of device
  * memory inside the library, one per GPU, held until the process ends; the call allocates and
  * frees nothing.  It serves every call whose qmlp_workspace_bytes(M, H, I, fmt) fits, e.g. M <= 32
- * at H = 5120, I = 17408; larger calls fail with QMLP_E_WORKSPACE.  The first call on a device
- * looks up the array's address and zeroes its arrival counters (a kernel on `stream`).  Every
- * call on one GPU shares that GPU's array: calls that overlap on one GPU (several streams or host
- * threads) race and must be serialised by the caller.  Arguments, constraints and results as
- * qmlp_forward_ex. */
+ * at H = 5120, I = 17408; larger calls fail with QMLP_E_WORKSPACE.  The array starts zeroed (it
+ * is loaded with the library's code object), and every forward leaves its arrival counters at
+ * zero.  The first call on a device looks up the array's address (hipGetSymbolAddress) and must
+ * be made outside graph capture: a first call on a capturing stream fails with QMLP_E_LAUNCH;
+ * later calls may be captured.  Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (several streams or host threads) race and must be serialised by the caller.
+ * Arguments, constraints and results as qmlp_forward_ex. */
 #define QMLP_SCRATCH_BYTES 33554432
 int qmlp_forward_noalloc(const void* x, const void* wg, const void* wu, const void* wd,
                          const void* residual, void* out, int M, int H, int I, int fmt, int flags,

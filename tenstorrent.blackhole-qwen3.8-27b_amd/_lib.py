@@ -1,9 +1,11 @@
 """ctypes binding of libqwen_mlp.so (the C ABI in include/qwen_mlp.h).
 
 The library is built in-tree by ``_build.py``.  There is no fallback: if the shared library is
-missing, every entry point raises.
+missing, every entry point raises, and so does a library whose source stamp (``qmlp_version()``)
+is not the digest of the sources beside it (a binary built from other sources).
 """
 import ctypes
+import importlib.util
 import os
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -57,8 +59,26 @@ class QmlpError(RuntimeError):
         self.code = code
 
 
+def _build_module():
+    spec = importlib.util.spec_from_file_location("_qmlp_build", os.path.join(PKG_DIR, "_build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def tree_source_hash():
+    """Digest of the kernel sources in this tree (what a build now would stamp)."""
+    return _build_module().source_hash()
+
+
+def library_source_hash(handle=None):
+    """The source digest stamped into the loaded library ("unstamped" if it has none)."""
+    version = (handle or lib()).qmlp_version().decode()
+    return version.rsplit("src=", 1)[1] if "src=" in version else "unstamped"
+
+
 def lib():
-    """Load libqwen_mlp.so (raises if it has not been built)."""
+    """Load libqwen_mlp.so (raises if it has not been built, or was built from other sources)."""
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
@@ -68,6 +88,10 @@ def lib():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
+        built, tree = library_source_hash(handle), tree_source_hash()
+        if built != tree:
+            raise RuntimeError(f"{LIB_PATH} was built from other sources (library src={built}, tree src={tree}): "
+                               "rebuild it with __graft_entry__.build()")
         _lib = handle
     return _lib
 

@@ -198,7 +198,12 @@ extern "C" {
 
 const char* qmlp_last_error(void) { return g_err; }
 
-const char* qmlp_version(void) { return "qwen_mlp 0.1 gfx950"; }
+// The build stamps the digest of the sources it compiled (see _build.py); a build without one
+// reports "unstamped".
+#ifndef QMLP_SOURCE_HASH
+#define QMLP_SOURCE_HASH "unstamped"
+#endif
+const char* qmlp_version(void) { return "qwen_mlp 0.3 gfx950 src=" QMLP_SOURCE_HASH; }
 
 size_t qmlp_packed_bytes(int rows, int cols, int fmt) {
   if (!shape_ok(rows, cols) || !known_fmt(fmt)) return 0;

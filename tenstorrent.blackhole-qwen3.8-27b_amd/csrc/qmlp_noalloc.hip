@@ -8,9 +8,12 @@
 // address with hipGetSymbolAddress and keeps it; every kernel argument and fill uses that address.
 //
 // Every call on one GPU shares that GPU's array and finds the previous call's contents in it.
-// Only the arrival counters must read zero when a forward starts: they are zeroed once per device
-// at set-up, and every forward leaves them zero.  Calls that overlap on one GPU (two streams, two
-// host threads) race on the array; callers serialise them.
+// Only the arrival counters must read zero when a forward starts: the array is zero when the code
+// object is loaded (a zero-initialised .bss section), and every forward leaves them zero, so no
+// call ever clears them.  The first call on a device must come from outside graph capture (the
+// address lookup may load the code object on that device); it is refused on a capturing stream.
+// Calls that overlap on one GPU (two streams, two host threads) race on the array; callers
+// serialise them.
 #include <mutex>
 
 #include "../../include/qwen_mlp.h"
@@ -25,8 +28,8 @@ static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
 
-// This device's address of `scratch`, looked up (and its counters zeroed on `s`) at the first call
-// on the device.  Thread-safe.
+// This device's address of `scratch`, looked up at the first call on the device (outside graph
+// capture).  Thread-safe.
 static int scratch_for_current_device(void** out, hipStream_t s) {
   static std::mutex mu;
   static void* addr[kMaxDevices] = {};
@@ -35,13 +38,17 @@ static int scratch_for_current_device(void** out, hipStream_t s) {
     return set_error(QMLP_E_DEVICE, "qmlp_forward_noalloc: no usable HIP device");
   std::lock_guard<std::mutex> lock(mu);
   if (!addr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess)
+      return set_error(QMLP_E_LAUNCH, "qmlp_forward_noalloc: cannot query the stream's capture status");
+    if (cs != hipStreamCaptureStatusNone)
+      return set_error(QMLP_E_LAUNCH,
+                       "qmlp_forward_noalloc: the first call on device %d must be made outside graph capture", dev);
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return set_error(QMLP_E_LAUNCH, "qmlp_forward_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
                        dev, hipGetErrorString(e));
-    // a kernel, not a memset node: the first call may itself be under graph capture
-    if (int rc = launch_fill_zero(p, QMLP_WS_COUNTER_BYTES, s)) return rc;
     addr[dev] = p;
   }
   *out = addr[dev];

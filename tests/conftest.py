@@ -14,7 +14,19 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
 
 
+def pytest_report_header(config):
+    """Names the library the session tests and the sources it was built from."""
+    try:
+        pkg = __graft_entry__.load_package()
+        from qwen_mlp_amd import _lib
+
+        return [f"libqwen_mlp: {pkg.lib().qmlp_version().decode()} (tree src={_lib.tree_source_hash()})"]
+    except Exception as e:  # a missing or stale library: the pkg fixture raises with the reason
+        return [f"libqwen_mlp: not loadable ({e})"]
+
+
 def _ensure_built():
+    """Builds a missing library; a stale one (stamped with other sources) makes pkg.lib() raise."""
     from importlib import import_module
 
     lib_path = os.path.join(__graft_entry__.PKG_DIR, "libqwen_mlp.so")

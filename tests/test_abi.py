@@ -32,6 +32,11 @@ def test_every_declared_symbol_is_exported(pkg):
 def test_version_and_error_strings(pkg):
     lib = pkg.lib()
     assert b"gfx950" in lib.qmlp_version()
+    from qwen_mlp_amd import _lib
+
+    # the loaded binary was built from exactly these sources (lib() refuses any other)
+    assert _lib.library_source_hash() == _lib.tree_source_hash()
+    assert re.fullmatch(r"[0-9a-f]{16}", _lib.tree_source_hash())
     assert lib.qmlp_forward(None, None, None, None, None, None, None, 0, 1, 256, 256, 1, None) == -6
     assert b"null" in lib.qmlp_last_error()
 
@@ -41,6 +46,16 @@ def test_version_and_error_strings(pkg):
 def test_packed_bytes_matches_layout(pkg, rows, cols, fmt):
     code = {"bfp8": pkg.FMT_BFP8, "bf4": pkg.FMT_BF4, "bf16": pkg.FMT_BF16}[fmt]
     assert pkg.lib().qmlp_packed_bytes(rows, cols, code) == obfp8.packed_bytes(rows, cols, fmt)
+
+
+def test_stale_library_is_refused(pkg, tmp_path, monkeypatch):
+    """A library whose stamp is not the digest of the sources beside it does not load."""
+    from qwen_mlp_amd import _lib
+
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "tree_source_hash", lambda: "0" * 16)
+    with pytest.raises(RuntimeError, match="built from other sources"):
+        _lib.lib()
 
 
 def test_packed_bytes_rejects_bad_shapes(pkg):
@@ -243,3 +258,31 @@ def test_bench_refuses_several_gpus():
                        text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_no_kernel_waits_for_another_block():
+    """Cross-block hand-offs are last-arrival only: no loop under csrc/ waits on a value in memory
+    (no loop condition reads memory, no sleep, no do-while), so every kernel finishes whatever else
+    holds the CUs."""
+    csrc = os.path.join(os.path.dirname(HEADER), "..", "tenstorrent.blackhole-qwen3.8-27b_amd", "csrc")
+    names = [n for n in os.listdir(csrc) if n.endswith((".hip", ".h"))]
+    assert len(names) >= 8
+    loops = 0
+    for name in names:
+        text = open(os.path.join(csrc, name)).read()
+        for m in re.finditer(r"\b(while|for)\s*\(", text):
+            depth, i = 1, m.end()
+            while depth:  # the condition up to its matching parenthesis
+                depth += {"(": 1, ")": -1}.get(text[i], 0)
+                i += 1
+            cond = text[m.end():i - 1]
+            if m.group(1) == "for":  # for (init; cond; step): the condition part
+                parts = cond.split(";")
+                if len(parts) != 3:
+                    continue
+                cond = parts[1]
+            loops += 1
+            assert not re.search(r"load|atomic|volatile|\[|->", cond), f"{name}: loop on memory ({cond})"
+        assert not re.search(r"\bdo\s*\{", text), f"{name}: do-while loop"
+        assert "s_sleep" not in text, name
+    assert loops > 100

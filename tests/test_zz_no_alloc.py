@@ -89,3 +89,75 @@ def test_noalloc_rejects_calls_beyond_the_scratch(pkg, cuda):
     rc = lib.qmlp_forward_noalloc(_lib.ptr(x16), _lib.ptr(w.w1.buf), _lib.ptr(w.w3.buf), _lib.ptr(w.w2.buf), None,
                                   _lib.ptr(o16), 16, 1024, 3072, 9, 0, _lib.stream_handle())
     assert rc == _lib.E_FORMAT
+
+
+def test_noalloc_captured_in_a_graph(pkg, cuda):
+    """After an eager first call on the device, no-allocation calls captured in a HIP graph replay
+    correctly: every replay (new inputs, eager work in between) equals the workspace entry point."""
+    import torch
+    from qwen_mlp_amd import _lib, workloads
+
+    lib = pkg.lib()
+    H, I, M = 1024, 3072, 16
+    w = pkg.load_mlp_weights(cuda, workloads.state_dict(H, I, layer=6, device=cuda), weight_format="bfp8")
+    x = workloads.activations(M, H, seed=1, device=cuda)
+    out = torch.empty_like(x)
+    assert _noalloc(lib, _lib, x, w, x, out, 0, _lib.stream_handle()) == 0, _lib.last_error()  # eager first call
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        rc = _noalloc(lib, _lib, x, w, x, out, 0, _lib.stream_handle(s))
+    assert rc == 0, _lib.last_error()
+    for seed in range(4):
+        new_x = workloads.activations(M, H, seed=400 + seed, device=cuda)
+        x.copy_(new_x)
+        g.replay()
+        torch.cuda.synchronize()
+        ref = torch.empty_like(x)
+        assert _with_workspace(lib, _lib, new_x, w, new_x, ref, 0, _lib.stream_handle(), pkg) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {seed} differs from the workspace entry point"
+
+
+def test_noalloc_first_call_under_capture_is_refused(pkg, cuda):
+    """In a fresh process, a first no-allocation call made while a graph captures is refused with
+    QMLP_E_LAUNCH (the address lookup must run eagerly); an eager call then succeeds."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = f"""
+import sys
+sys.path.insert(0, {root!r})
+import torch
+import __graft_entry__
+pkg = __graft_entry__.load_package()
+from qwen_mlp_amd import _lib, workloads
+lib = pkg.lib()
+dev = torch.device("cuda:0")
+w = pkg.load_mlp_weights(dev, workloads.state_dict(1024, 3072, layer=6, device=dev), weight_format="bfp8")
+x = workloads.activations(16, 1024, seed=1, device=dev)
+out = torch.empty_like(x)
+args = lambda st: (_lib.ptr(x), _lib.ptr(w.w1.buf), _lib.ptr(w.w3.buf), _lib.ptr(w.w2.buf), _lib.ptr(x),
+                   _lib.ptr(out), 16, 1024, 3072, w.w1.fmt_code, 0, st)
+torch.cuda.synchronize()
+s = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):
+    rc = lib.qmlp_forward_noalloc(*args(_lib.stream_handle(s)))
+    msg = _lib.last_error()
+rc2 = lib.qmlp_forward_noalloc(*args(_lib.stream_handle()))
+torch.cuda.synchronize()
+print("RESULT", rc, rc2, msg, flush=True)
+"""
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    line = [l for l in res.stdout.splitlines() if l.startswith("RESULT")]
+    assert res.returncode == 0 and line, res.stdout + res.stderr
+    _, rc, rc2, msg = line[0].split(" ", 3)
+    from qwen_mlp_amd import _lib
+
+    assert int(rc) == _lib.E_LAUNCH and "outside graph capture" in msg
+    assert int(rc2) == 0
