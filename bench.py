@@ -118,9 +118,10 @@ def copy_calibration(mib, device):
     del a, b
 
 
-# The sources that decide what the M <= 32 gate/up kernel reads and writes: a traffic figure
-# measured on other sources describes another kernel.
-TRAFFIC_SOURCES = ("qmlp_gemv.hip", "qmlp_common.h", "qmlp_internal.h", "qmlp_abi.hip")
+# The sources that decide what the M <= 32 weight-streaming kernels read and write (their code,
+# the packed layout and dequantisation helpers): a traffic figure measured on other sources
+# describes other kernels.
+TRAFFIC_SOURCES = ("qmlp_gemv.hip", "qmlp_common.h")
 
 
 def kernel_source_hash():
@@ -135,13 +136,17 @@ def kernel_source_hash():
     return h.hexdigest()[:16]
 
 
-def read_traffic(workload):
-    """HBM bytes per launch of the gate/up kernel from the committed counter summary.
+TRAFFIC_FILE = os.path.join("profiles", "gemv_m16_bfp8_traffic.md")
 
-    Returns (bytes or None, note).  The summary is used only when it names this workload and was
-    measured on the current kernel sources (its ``kernel_source_sha256`` line); otherwise the bench
-    line reports no traffic rather than a stale figure."""
-    path = os.path.join(ROOT, "profiles", "gemv_gate_up_m16_bfp8_traffic.md")
+
+def read_traffic(workload):
+    """HBM bytes per launch of the gate/up and down kernels from the committed counter summary.
+
+    Returns ({"gate_up": bytes, "down": bytes} or None, note).  The summary is used only when it
+    names this workload and was measured on the current kernel sources (its
+    ``kernel_source_sha256`` line); otherwise the bench line reports no traffic rather than a stale
+    figure."""
+    path = os.path.join(ROOT, TRAFFIC_FILE)
     if not os.path.exists(path):
         return None, "no counter summary"
     vals = {}
@@ -155,7 +160,8 @@ def read_traffic(workload):
     if vals.get("kernel_source_sha256") != kernel_source_hash():
         return None, "counter summary was measured on other kernel sources"
     try:
-        return int(vals["hbm_bytes_per_launch"]), "profiles/gemv_gate_up_m16_bfp8_traffic.md"
+        return {"gate_up": int(vals["hbm_bytes_per_launch_gate_up"]),
+                "down": int(vals["hbm_bytes_per_launch_down"])}, TRAFFIC_FILE
     except (KeyError, ValueError):
         return None, "counter summary has no byte count"
 
@@ -229,7 +235,10 @@ def main():
     import __graft_entry__
 
     pkg = __graft_entry__.load_package()
-    from qwen_mlp_amd import workloads
+    from qwen_mlp_amd import _lib, workloads
+
+    library_hash = _lib.library_source_hash()  # lib() has refused a binary built from other sources
+    _log(f"library {pkg.lib().qmlp_version().decode()}")
 
     dev = torch.device("cuda:0")
     wl = workloads.WORKLOADS[args.workload]
@@ -250,6 +259,7 @@ def main():
     gu_ms = kern["gate_up"]
     gu_gbs = gu_bytes / (gu_ms / 1e3) / 1e9
     traffic, traffic_src = read_traffic(wl.name)
+    dn_bytes = wl.algorithmic_bytes() - gu_bytes  # down weights + the out write (W + 4 M H in all)
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -272,8 +282,16 @@ def main():
         "kernel_ms": {k: round(v, 5) for k, v in kern.items()},
         "roofline": {"kernel": "gate/up projection (gemv_kernel, 2 matrices)", "bound": "hbm",
                      "achieved": round(gu_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
-                     "kernel_source_sha256": kernel_source_hash(), "algorithmic_bytes_per_launch": gu_bytes},
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["gate_up"] if traffic else None, "traffic_source": traffic_src,
+                     "traffic_over_algorithmic": round(traffic["gate_up"] / gu_bytes, 4) if traffic else None,
+                     "kernel_source_sha256": kernel_source_hash(), "algorithmic_bytes_per_launch": gu_bytes,
+                     "down": {"achieved": round(dn_bytes / (kern["down"] / 1e3) / 1e9, 2),
+                              "frac": round(dn_bytes / (kern["down"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "algorithmic_bytes_per_launch": dn_bytes,
+                              "traffic": traffic["down"] if traffic else None,
+                              "traffic_over_algorithmic": round(traffic["down"] / dn_bytes, 4) if traffic else None}},
+        "library_source_sha16": library_hash,
     }
     if wl.tokens > 32:  # many-token chunks run the matrix-core kernels: bound by the MFMA peak
         gu_flops = 4 * wl.tokens * wl.hidden * wl.intermediate

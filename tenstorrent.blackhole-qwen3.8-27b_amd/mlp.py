@@ -206,18 +206,37 @@ def new_workspace(M, H, I, fmt, device, stream=None):
     return _new_workspace_bytes(workspace_bytes(M, H, I, fmt), device, stream)
 
 
+def graph_capture_stream(device=None):
+    """The stream ``torch.cuda.graph(g)`` captures on when it is given no ``stream``: torch's
+    ``torch.cuda.graph.default_capture_stream``, created here the way torch creates it (lazily, one
+    per process) if no graph has been built yet."""
+    cls = torch.cuda.graphs.graph
+    if cls.default_capture_stream is None:
+        with torch.cuda.device(device):
+            cls.default_capture_stream = torch.cuda.Stream()
+    return cls.default_capture_stream
+
+
 class WorkspacePool:
     """One forward workspace per (device, stream), shared by every MLP that runs there.
 
     Forwards on one stream run one after another, so they can share a workspace.  Forwards on
     different streams may overlap, so each stream gets its own.  A workspace only grows, and only
     outside graph capture: during a capture the stream must already hold a large enough one.  Run
-    one forward on that stream first, or call ``reserve``.  The reference keeps one scratch buffer
-    per device for all layers in the same way (``docker/qwen-c2-graft/graft/mlp.py:274-356``).
+    one forward on that stream first, or call ``reserve`` (``Qwen36MLP`` reserves for the current
+    stream and for the stream ``torch.cuda.graph`` captures on by default).  The reference keeps one
+    scratch buffer per device for all layers in the same way
+    (``docker/qwen-c2-graft/graft/mlp.py:274-356``).
+
+    A workspace replaced by a larger one is kept alive, not freed: a HIP graph captured before the
+    growth still addresses it, and its replays must not write into memory the caching allocator has
+    handed to other tensors.  ``clear()`` drops every workspace, the replaced ones included; call it
+    only once no captured graph that used them will be replayed.
     """
 
     def __init__(self):
         self._ws = {}
+        self._retired = []
 
     @staticmethod
     def _key(device, stream):
@@ -235,8 +254,9 @@ class WorkspacePool:
                                  "forward on the capturing stream before capturing, or call WorkspacePool.reserve")
             if ws is not None:
                 nbytes = max(nbytes, ws.numel())
-            # allocated with the stream current, so that the caching allocator hands the memory of a
-            # replaced workspace only to later work on this stream (stream-ordered after its last use)
+                self._retired.append(ws)  # a graph captured earlier may still address it
+            # allocated with the stream current, so that the caching allocator keeps the new memory
+            # stream-ordered with this stream's work
             s = stream if stream is not None else torch.cuda.current_stream(device)
             with torch.cuda.stream(s):
                 ws = _new_workspace_bytes(nbytes, device, s)
@@ -244,10 +264,17 @@ class WorkspacePool:
         return ws
 
     def total_bytes(self):
+        """Bytes of the live workspaces (the replaced ones kept for captured graphs not counted)."""
         return sum(ws.numel() for ws in self._ws.values())
 
+    def retired_bytes(self):
+        """Bytes of replaced workspaces kept alive for graphs captured before a growth."""
+        return sum(ws.numel() for ws in self._retired)
+
     def clear(self):
+        """Drop every workspace, the replaced ones included (no captured graph may use them again)."""
         self._ws.clear()
+        self._retired.clear()
 
 
 # Shared by every Qwen36MLP unless one is given its own pool.
@@ -431,9 +458,10 @@ class Qwen36MLP:
     weight_format="bfp8", max_tokens=2048, pool=None)``; ``forward(x, residual=None, out=None)``.
     Every instance takes its workspace from ``pool`` (the module's shared ``workspace_pool`` by
     default): one workspace per (device, stream) for all layers, reserved here for up to
-    ``max_tokens`` rows on the current stream.  ``forward`` allocates nothing but its output (and
-    nothing at all when ``out`` is given), so it may run inside a HIP graph capture on a stream that
-    already holds a large enough workspace.
+    ``max_tokens`` rows on the current stream and on the stream ``torch.cuda.graph`` captures on by
+    default.  ``forward`` allocates nothing but its output (and nothing at all when ``out`` is
+    given), so it may run inside a HIP graph capture on a stream that already holds a large enough
+    workspace.
     """
 
     def __init__(self, mesh_device, state_dict, tensor_cache_path=None, args=None, tt_ccl=None,
@@ -444,7 +472,13 @@ class Qwen36MLP:
         self.weights = load_mlp_weights(self.device, state_dict, tensor_cache_path, args, weight_format)
         self.max_tokens = int(max_tokens)
         self.pool = workspace_pool if pool is None else pool
-        self.pool.reserve(self._workspace_bytes(self.max_tokens), self.device)
+        nbytes = self._workspace_bytes(self.max_tokens)
+        self.pool.reserve(nbytes, self.device)
+        # torch.cuda.graph(g) without a stream captures on its own side stream: give it a workspace
+        # too, so that the usual warm-up-then-capture pattern needs no stream argument
+        cap = graph_capture_stream(self.device)
+        if cap.device == self.device or (cap.device.index is None and self.device.index in (None, 0)):
+            self.pool.reserve(nbytes, self.device, cap)
 
     @property
     def weight_format(self):

@@ -1,6 +1,9 @@
 """Shared helpers of the GPU parity tests: identically dequantised host weights, the oracle call
 and the stated bar (max|out - oracle| <= 1e-2 * RMS(oracle); a bf16 output also gets half a bf16
 ulp of the oracle value)."""
+import json
+import os
+
 import numpy as np
 
 from oracle import bf16 as obf16
@@ -8,6 +11,19 @@ from oracle import bfp8 as obfp8
 from oracle import mlp as omlp
 
 TOL = 1e-2
+
+# With QMLP_MARGINS=<path>, every check appends one JSON line {test, what, kind, ratio} (ratio =
+# error / bar; a case passes at <= 1), so a run leaves the margin of every parity case behind.
+MARGINS_ENV = "QMLP_MARGINS"
+
+
+def record_margin(what, kind, ratio):
+    path = os.environ.get(MARGINS_ENV)
+    if not path:
+        return
+    test = os.environ.get("PYTEST_CURRENT_TEST", "").split(" (")[0]
+    with open(path, "a") as f:
+        f.write(json.dumps({"test": test, "what": what, "kind": kind, "ratio": round(float(ratio), 4)}) + "\n")
 
 
 def bits(t):
@@ -40,6 +56,7 @@ def check(y, ref, what):
     """The stated bar on an fp32 (unrounded) output; returns err / bound."""
     ok, err, bound = omlp.tolerance_ok(y, ref, TOL)
     print(f"{what}: max|err|={err:.4e} bound={bound:.4e} ({err / bound:.2f} of the bar)", flush=True)
+    record_margin(what, "fp32", err / bound if bound > 0 else (0.0 if err == 0 else float("inf")))
     assert ok, f"{what}: {err} > {bound}"
     return err / bound
 
@@ -49,6 +66,7 @@ def check_bf16(y, ref, what):
     |y - ref| <= 1e-2 * RMS(ref) + half a bf16 ulp of ref."""
     ok, worst, bound = omlp.tolerance_ok_bf16(y, ref, TOL)
     print(f"{what} (bf16 out): max(|err| - half ulp)={worst:.4e} bar={bound:.4e}", flush=True)
+    record_margin(what, "bf16", max(worst, 0.0) / bound if bound > 0 else 0.0)
     assert ok, f"{what}: {worst} > {bound}"
 
 
@@ -76,5 +94,6 @@ def check_rows(y, ref, what, bf16_out=False):
     ratio = np.max(dev, axis=1) / (TOL * np.maximum(rms, 1e-300))
     worst = float(np.max(ratio))
     print(f"{what}: worst row at {worst:.2f} of the per-row bar (row {int(np.argmax(ratio))})", flush=True)
+    record_margin(what, "row-bf16" if bf16_out else "row-fp32", worst)
     assert worst <= 1.0, f"{what}: row {int(np.argmax(ratio))} at {worst:.3f} of the bar"
     return worst

@@ -523,10 +523,15 @@ def test_offline_packer_round_trip(pkg, cuda, tmp_path, fmt):
         assert np.array_equal(np.load(d / "down_proj.q.npy", mmap_mode="r"), q.cpu().numpy())
 
 
-def test_verify_arm_routes_decoder_mlps(pkg, cuda):
+@pytest.mark.parametrize("rows", [16, 32])
+def test_verify_arm_routes_decoder_mlps(pkg, cuda, rows):
     """A toy 2-layer decoder (norm -> MLP -> residual, layer.py:352-357, attention left out) whose
-    feed-forward modules are plain torch MLPs: inside the arm's scope the verify-width calls run the
-    library and match the torch path, other widths fall back, and the bindings come back."""
+    feed-forward modules are plain torch MLPs: inside the arm's scope the verify-width calls (16 or
+    32 token rows, the reference's T16 and T32 arms) run the library and match the torch path,
+    other widths fall back, and the bindings come back.  Before the first scope the arm checks
+    each layer's packed weights byte for byte against that layer's own (2 x 3 matrices)."""
+    import types
+
     import torch
     from qwen_mlp_amd import verify_arm, workloads
 
@@ -534,11 +539,13 @@ def test_verify_arm_routes_decoder_mlps(pkg, cuda):
 
     class TorchMLP:
         def __init__(self, sd):
-            self.g, self.u, self.d = (sd[f"{k}.weight"].float() for k in ("gate_proj", "up_proj", "down_proj"))
+            for k in ("gate_proj", "up_proj", "down_proj"):
+                setattr(self, k, types.SimpleNamespace(weight=sd[f"{k}.weight"]))
 
         def forward(self, x):
             xf = x.float()
-            return ((torch.nn.functional.silu(xf @ self.g.T) * (xf @ self.u.T)) @ self.d.T).to(torch.bfloat16)
+            g, u, d = (getattr(self, k).weight.float() for k in ("gate_proj", "up_proj", "down_proj"))
+            return ((torch.nn.functional.silu(xf @ g.T) * (xf @ u.T)) @ d.T).to(torch.bfloat16)
 
     class ToyLayer:
         def __init__(self, mlp):
@@ -551,34 +558,48 @@ def test_verify_arm_routes_decoder_mlps(pkg, cuda):
 
     sds = [workloads.state_dict(H, I, layer=30 + i, device=cuda) for i in range(2)]
     layers = [ToyLayer(TorchMLP(sd)) for sd in sds]
-    amd = [pkg.Qwen36MLP(cuda, sd, weight_format="bf16", max_tokens=16) for sd in sds]
-    arm = verify_arm.VerifyArm([l.feed_forward for l in layers], amd, token_rows=16)
+    amd = [pkg.Qwen36MLP(cuda, sd, weight_format="bf16", max_tokens=rows) for sd in sds]
+    arm = verify_arm.VerifyArm([l.feed_forward for l in layers], amd, token_rows=rows)
 
     def run(h):
         for layer in layers:
             h = layer.forward(h)
         return h
 
-    h16 = workloads.activations(16, H, seed=4, device=cuda).view(1, 1, 16, H)
+    hv = workloads.activations(rows, H, seed=4, device=cuda).view(1, 1, rows, H)
     h8 = workloads.activations(8, H, seed=5, device=cuda).view(1, 1, 8, H)
-    ref16, ref8 = run(h16), run(h8)
+    refv, ref8 = run(hv), run(h8)
     with arm.install():
-        out16, out8 = run(h16), run(h8)
+        outv, out8 = run(hv), run(h8)
     torch.cuda.synchronize()
-    assert arm.audit == dict(rows=16, layers=2, hits=[1, 1], fallbacks=[1, 1], restored=True,
-                          weights_unchanged=True)
+    assert arm.audit == dict(rows=rows, layers=2, hits=[1, 1], fallbacks=[1, 1], restored=True,
+                             weights_unchanged=True, weights_checked=6)
+    assert len(arm.weight_checks) == 6 and all(c["exact"] for c in arm.weight_checks)
     assert torch.equal(out8, ref8)  # fell back to the torch path
     # The torch decoder rounds the MLP output to bf16 before the residual add, the library rounds
     # the sum once: besides the 1e-2 * RMS bar allow two bf16 ulps of the reference per element.
-    y = out16.double().reshape(16, H).cpu().numpy()
-    r = ref16.double().reshape(16, H).cpu().numpy()
+    y = outv.double().reshape(rows, H).cpu().numpy()
+    r = refv.double().reshape(rows, H).cpu().numpy()
     _, e = np.frexp(np.abs(r))
     excess = float(np.max(np.abs(y - r) - 2 * np.ldexp(1.0, e - 8)))
     bar = TOL * float(np.sqrt(np.mean(r * r)))
-    print(f"verify arm vs torch decoder: max(|err| - 2 ulp)={excess:.4e} bar={bar:.4e}", flush=True)
+    print(f"verify arm T{rows} vs torch decoder: max(|err| - 2 ulp)={excess:.4e} bar={bar:.4e}", flush=True)
     assert excess <= bar
     assert all("forward" not in l.feed_forward.__dict__ for l in layers)
     with pytest.raises(ZeroDivisionError):
         with arm.install():
             1 / 0
     assert arm.audit["restored"] and not arm.active
+    # a swapped pairing (layer 0's library weights serving layer 1 and back) is refused, unbound
+    swapped = verify_arm.VerifyArm([l.feed_forward for l in layers], amd[::-1], token_rows=rows)
+    with pytest.raises(ValueError, match="layer 0: the library's packed gate_proj is not this decoder layer"):
+        with swapped.install():
+            pytest.fail("a swapped pairing must not install")
+    assert all("forward" not in l.feed_forward.__dict__ for l in layers) and not swapped.active
+    # one stale matrix (layer 1's down projection re-packed from other weights) is refused too
+    stale = pkg.Qwen36MLP(cuda, dict(sds[1], **{"down_proj.weight": sds[0]["down_proj.weight"]}),
+                          weight_format="bf16", max_tokens=rows)
+    bad = verify_arm.VerifyArm([l.feed_forward for l in layers], [amd[0], stale], token_rows=rows)
+    with pytest.raises(ValueError, match="layer 1: the library's packed down_proj"):
+        bad.__enter__()
+    assert not bad.active
