@@ -36,3 +36,23 @@ def f32_to_bits(values, ties_away=False):
 def round_f32(values):
     """Round float32 values to the nearest bf16 value (nearest-even) and return them as float32."""
     return bits_to_f32(f32_to_bits(values))
+
+
+def round_f64(values):
+    """Round float64 values to the nearest bf16 value (nearest-even) once, returned as float64.
+
+    Going through float32 with nearest-even would round twice and can land on a bf16 tie that the
+    float64 value does not sit on.  The float32 step here rounds to odd instead (truncate toward
+    zero, then set the last bit when anything was cut off), which keeps the later nearest-even
+    rounding to bf16 exact because float32 carries more than two bits beyond bf16's 8 (Boldo and
+    Melquiond, "Emulation of FMA and correctly rounded sums: proved algorithms using rounding to
+    odd", IEEE Trans. Computers 57(4), 2008).  Finite inputs within the float32 range only.
+    """
+    v = np.asarray(values, dtype=np.float64)
+    t = v.astype(np.float32)
+    away = np.abs(t.astype(np.float64)) > np.abs(v)
+    t = np.where(away, np.nextafter(t, np.float32(0)), t).astype(np.float32)  # truncated toward zero
+    inexact = t.astype(np.float64) != v
+    words = t.view(np.uint32) | inexact.astype(np.uint32)  # round to odd
+    return round_f32(words.view(np.float32)).astype(np.float64)
+

@@ -31,21 +31,39 @@ def epilogue_h_bf16(g, u):
     return obf16.round_f32(silu(g) * u)
 
 
-def swiglu(x, wg, wu, wd, residual=None, h_bf16=False):
-    """``residual + down(silu(gate(x)) * up(x))`` in float32.
+def round_fp16_significand(v):
+    """Round values to fp16's 11 significant bits (nearest-even) with an unbounded exponent range,
+    in float64.  Equal to fp16 rounding for every value in fp16's normal range and, as a power-of-two
+    scale commutes with such rounding, to the block-float kernels' h = fp16(h * 2^th) * 2^-th for
+    every h that their per-token th keeps normal."""
+    v = np.asarray(v, dtype=np.float64)
+    m, e = np.frexp(v)  # v = m * 2^e, 0.5 <= |m| < 1
+    return np.ldexp(np.rint(np.ldexp(m, 11)), e - 11)
+
+
+def swiglu(x, wg, wu, wd, residual=None, h_bf16=False, dtype=np.float32):
+    """``residual + down(silu(gate(x)) * up(x))`` in float32 (or in ``dtype``).
 
     x: [M, H]; wg, wu: [I, H] (out, in); wd: [H, I]; residual: [M, H] or None.  With ``h_bf16`` the
     intermediate h is rounded to bf16 once (``epilogue_h_bf16``) before the down projection, as the
-    bf16-weight path and the reference's fused gate/up keep it.
+    bf16-weight path and the reference's fused gate/up keep it.  ``dtype=np.float64`` evaluates
+    the same formula in double precision (the bf16 rounding of h then rounds the double product):
+    on heavy-tailed data, where the float32 formula's own rounding is a sizeable part of a 1e-2
+    bar, it stands in for exact arithmetic.  The result is returned as float32 either way.
     Follows ``scripts/ci/mlp-sweep.py:121-126`` and ``layer.py:357``.
     """
-    x = np.asarray(x, dtype=np.float32)
-    g = x @ np.asarray(wg, dtype=np.float32).T
-    u = x @ np.asarray(wu, dtype=np.float32).T
-    h = epilogue_h_bf16(g, u) if h_bf16 else silu(g) * u
-    y = h @ np.asarray(wd, dtype=np.float32).T
+    x = np.asarray(x, dtype=dtype)
+    g = x @ np.asarray(wg, dtype=dtype).T
+    u = x @ np.asarray(wu, dtype=dtype).T
+    if h_bf16:
+        from . import bf16 as obf16
+
+        h = obf16.round_f64(silu(g) * u) if dtype == np.float64 else epilogue_h_bf16(g, u)
+    else:
+        h = silu(g) * u
+    y = h @ np.asarray(wd, dtype=dtype).T
     if residual is not None:
-        y = y + np.asarray(residual, dtype=np.float32)
+        y = y + np.asarray(residual, dtype=dtype)
     return y.astype(np.float32)
 
 

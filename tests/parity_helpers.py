@@ -47,9 +47,9 @@ def host_weights(pkg, sd, fmt):
             for name in ("gate_proj", "up_proj", "down_proj")}
 
 
-def oracle(xf, hw, residual=True, h_bf16=False):
+def oracle(xf, hw, residual=True, h_bf16=False, dtype=np.float32):
     return omlp.swiglu(xf, hw["gate_proj"], hw["up_proj"], hw["down_proj"], residual=xf if residual else None,
-                       h_bf16=h_bf16)
+                       h_bf16=h_bf16, dtype=dtype)
 
 
 def check(y, ref, what):
@@ -97,3 +97,62 @@ def check_rows(y, ref, what, bf16_out=False):
     record_margin(what, "row-bf16" if bf16_out else "row-fp32", worst)
     assert worst <= 1.0, f"{what}: row {int(np.argmax(ratio))} at {worst:.3f} of the bar"
     return worst
+
+
+
+def fp16_h_reference(xf, hw):
+    """The output with h rounded to fp16's significand, and the per-element allowance for the
+    places where the kernels' fp32 h may legitimately round the other way.
+
+    The kernels compute h in fp32 (products exact, fp32 sums, SiLU through the hardware exp2 and
+    reciprocal) and round h * 2^th to fp16.  Where the exact h lies within that fp32 error of an
+    fp16 rounding midpoint, the kernel may round to the other neighbour: one fp16 ulp.  The fp32
+    error is taken as 2^-24 (16 + 2 sqrt(K) (sum|x w_g| / |g| + sum|x w_u| / |u|)) relative (sums
+    of K products: about sqrt(K) ulp of the absolute sum, 2x that here; SiLU and the products a
+    few ulp).  Values that scale into fp16's subnormal range (|h| 2^th < 2^-13, th from the
+    Cauchy-Schwarz bound, one binade wide of the kernels' own) may be flushed or lose bits: their
+    whole value is allowed.  Returns (y_fp16h [M, H] float64, allowance [M, H] float64)."""
+    x = np.asarray(xf, np.float64)
+    wg, wu, wd = (np.asarray(hw[n], np.float64) for n in ("gate_proj", "up_proj", "down_proj"))
+    g, u = x @ wg.T, x @ wu.T
+    ax = np.abs(x)
+    cg, cu = ax @ np.abs(wg).T, ax @ np.abs(wu).T
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        h = g / (1.0 + np.exp(-g)) * u
+        rel = 2.0 ** -24 * (16 + 2 * np.sqrt(x.shape[1]) * (cg / np.abs(g) + cu / np.abs(u)))
+    rel = np.where(np.isfinite(rel), rel, np.inf)
+    hr = omlp.round_fp16_significand(h)
+    m, e = np.frexp(h)
+    ulp = np.ldexp(1.0, e - 11)
+    t = np.abs(np.ldexp(m, 11))
+    mid_dist = np.abs(t - np.floor(t) - 0.5) * ulp  # distance to the nearest midpoint
+    near_tie = mid_dist <= rel * np.abs(h)
+    gn = np.sqrt((wg * wg).sum(1)).max()
+    un = np.sqrt((wu * wu).sum(1)).max()
+    bound = (x * x).sum(1) * gn * un * (1 + 1 / 64)
+    th = np.where(bound > 0, 15 - np.frexp(bound)[1], 0)
+    tiny = np.abs(h) < np.ldexp(1.0, -13 - th)[:, None]
+    slack = np.where(tiny, np.abs(h) + ulp, np.where(near_tie, ulp, 0.0))
+    return hr @ wd.T, slack @ np.abs(wd).T
+
+
+def check_fp16_h(y, xf, hw, what, frac=0.02, per_row=False):
+    """The kernels' bare MLP output (no residual) against the fp16-h formula (``fp16_h_reference``):
+    every element within its rounding-tie allowance plus ``frac`` of the bar (1e-2 x RMS of the
+    exact output, or of its token row with ``per_row``).  This separates the one specified rounding
+    of h from everything else the kernels do."""
+    y = np.asarray(y, np.float64)
+    y16, allow = fp16_h_reference(xf, hw)
+    exact = oracle(xf, hw, residual=False, dtype=np.float64).astype(np.float64)
+    if per_row:
+        bar = TOL * np.maximum(np.sqrt(np.mean(exact * exact, axis=1, keepdims=True)), 1e-300)
+    else:
+        bar = TOL * np.sqrt(np.mean(exact * exact))
+    over = float(np.max((np.abs(y - y16) - allow) / bar))
+    raw = float(np.max(np.abs(y - y16) / bar))
+    print(f"{what} vs the fp16-h formula: {raw:.4f} of the bar, {over:.4f} beyond the tie allowance "
+          f"(allowed {frac})", flush=True)
+    record_margin(what, "fp16-h", max(over, 0.0) / frac)
+    record_margin(what, "fp16-h-raw", raw)  # information only: the distance before the tie allowance
+    assert over <= frac, f"{what}: {over:.4f} of the bar beyond the fp16-h formula's tie allowance"
+    return over

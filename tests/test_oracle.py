@@ -273,6 +273,68 @@ def test_swiglu_matches_float64_brute_force():
     assert np.allclose(got, ref, rtol=2e-5, atol=2e-5)
 
 
+def test_swiglu_float64_matches_brute_force_to_double_precision():
+    # the float64 evaluation is the same formula: against the Python-float brute force it agrees
+    # to double rounding, and it moves away from the float32 evaluation by float32's error only
+    x, wg, wu, wd, res = _small(11)
+    ref = _brute(x, wg, wu, wd, res)
+    got64 = omlp.swiglu(x, wg, wu, wd, residual=res, dtype=np.float64)
+    assert got64.dtype == np.float32
+    assert np.allclose(got64, ref, rtol=0, atol=4e-7 * np.abs(ref).max())  # float32 output rounding
+    got32 = omlp.swiglu(x, wg, wu, wd, residual=res)
+    assert not np.array_equal(got32, got64) and np.allclose(got32, got64, rtol=2e-5, atol=2e-5)
+
+
+def _nearest_bf16(v):
+    """Brute force: the bf16 neighbours of float64 v (exhaustive over the two candidates of its
+    exponent), nearest, ties to the even word."""
+    lo = int(bf16.f32_to_bits(np.array([v], np.float32))[0])  # some nearby word
+    best = None
+    for w in range(lo - 2, lo + 3):
+        c = float(bf16.bits_to_f32(np.array([w & 0xFFFF], np.uint16))[0])
+        key = (abs(c - v), w & 1)
+        if best is None or key < best[0]:
+            best = (key, c)
+    return best[1]
+
+
+def test_round_f64_rounds_once():
+    # a value just above a bf16 tie rounds up; through float32 nearest-even it would land on the
+    # tie and go to the even word (1.0)
+    assert bf16.round_f64(np.array([1 + 2.0 ** -8 + 2.0 ** -30]))[0] == 1.0078125
+    assert float(bf16.round_f32(np.float32(1 + 2.0 ** -8 + 2.0 ** -30))) == 1.0  # the double rounding
+    assert bf16.round_f64(np.array([1 + 2.0 ** -8]))[0] == 1.0  # an exact tie: even
+    assert bf16.round_f64(np.array([1 + 3 * 2.0 ** -8]))[0] == 1.015625
+    rng = np.random.RandomState(3)
+    v = rng.standard_normal(3000) * np.exp2(rng.randint(-20, 20, 3000))
+    ties = bf16.bits_to_f32(bf16.f32_to_bits(v[:500].astype(np.float32))).astype(np.float64)
+    v[:500] = ties * (1 + 2.0 ** -9 * np.sign(rng.standard_normal(500)))  # near the midpoints
+    v[500:700] = ties[:200] * (1 + 2.0 ** -9) + rng.choice([-1, 1], 200) * np.abs(ties[:200]) * 2.0 ** -40
+    got = bf16.round_f64(v)
+    assert all(got[i] == _nearest_bf16(v[i]) for i in range(v.size))
+
+
+def test_swiglu_float64_rounds_h_once_to_bf16():
+    x, wg, wu, wd, _ = _small(12)
+    x64, g64, u64, d64 = (a.astype(np.float64) for a in (x, wg, wu, wd))
+    g, u = x64 @ g64.T, x64 @ u64.T
+    h = np.vectorize(_nearest_bf16)(g / (1 + np.exp(-g)) * u)
+    want = (h @ d64.T).astype(np.float32)
+    assert np.array_equal(omlp.swiglu(x, wg, wu, wd, h_bf16=True, dtype=np.float64), want)
+
+
+def test_round_fp16_significand_is_fp16_rounding_in_the_normal_range():
+    # numpy's float16 conversion rounds to nearest-even: the two agree on every normal value, and
+    # a power-of-two scale commutes with the significand rounding
+    rng = np.random.RandomState(7)
+    v = rng.standard_normal(20000) * np.exp2(rng.uniform(-13, 15, 20000))
+    v = v[(np.abs(v) < 65504) & (np.abs(v) >= 2.0 ** -14)]  # the normal range
+    assert np.array_equal(omlp.round_fp16_significand(v), v.astype(np.float16).astype(np.float64))
+    ties = np.array([1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -(1 + 2.0 ** -11)])  # halfway: even
+    assert np.array_equal(omlp.round_fp16_significand(ties), [1.0, 1 + 2.0 ** -9, -1.0])
+    assert np.array_equal(omlp.round_fp16_significand(v * 2.0 ** -40), omlp.round_fp16_significand(v) * 2.0 ** -40)
+
+
 def test_swiglu_matches_c_oracle_and_torch_float64():
     torch = pytest.importorskip("torch")
     x, wg, wu, wd, res = _small(2, M=5, H=64, I=96)
