@@ -620,11 +620,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
   }
   __syncthreads();
 
-  // publish this workgroup's per-tile partial sums
+  // publish this workgroup's per-tile partial sums.  Wave w publishes tiles w, w + NW, ... and,
+  // if this workgroup arrives last, finishes the same tiles: it keeps the first kEpt of its sums
+  // in registers and adds them in place of re-reading its own slots.
   const int m = lane & 15;
   const __amdgpu_buffer_rsrc_t prs = part_rsrc(p, SLOT);
-  for (int tl = wave; tl < Gw; tl += NW) {
-    f32x4 sum[NMAT][MG];
+  f32x4 own[kEpt][NMAT][MG];
+  auto publish = [&](int tl, f32x4 (&sum)[NMAT][MG]) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
@@ -653,6 +655,13 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
       for (int mg = 0; mg < MG; ++mg) store_coherent(prs, dst + (mat * MG + mg) * 1024u, sum[mat][mg]);
+  };
+#pragma unroll
+  for (int k = 0; k < kEpt; ++k)
+    if (wave + k * NW < Gw) publish(wave + k * NW, own[k]);
+  for (int tl = wave + kEpt * NW; tl < Gw; tl += NW) {
+    f32x4 sum[NMAT][MG];
+    publish(tl, sum);
   }
   if (p.x_scale && threadIdx.x < ROWS)
     __hip_atomic_store(p.pss + (size_t)w * kPssStride + threadIdx.x, s_ss[threadIdx.x], __ATOMIC_RELAXED,
@@ -689,6 +698,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
     const int tl = min(wave + k * NW, Gw - 1);
 #pragma unroll
     for (int qq = 0; qq < QB; ++qq) {
+      if (qq == q) continue;  // this workgroup's own split: in registers (q is uniform)
       const uint32_t src = slot_src(qq, tl);
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat)
@@ -722,17 +732,20 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
       if (g == 0 && wave == 0 && lane < 16 && mg * 16 + lane < p.M) p.th_out[mg * 16 + lane] = th[mg];
     }
   }
-  // slots q0.. of tile tl, added in K order, two splits per round trip (more than QB splits)
-  auto sum_rest = [&](int tl, int q0, f32x4 (&tot)[NMAT][MG]) {
+  // slots q0.. of tile tl, added in K order, two splits per round trip (more than QB splits);
+  // ow: this workgroup's own sum of the tile, when kept (used in place of its slot)
+  auto sum_rest = [&](int tl, int q0, f32x4 (&tot)[NMAT][MG], const f32x4 (*ow)[MG]) {
     for (int qb = q0; qb < p.S; qb += 2) {
       f32x4 u[2][NMAT][MG];
 #pragma unroll
       for (int qq = 0; qq < 2; ++qq) {
         const uint32_t src = slot_src(qb + qq, tl);
+        const bool mine = ow != nullptr && qb + qq == q;
 #pragma unroll
         for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-          for (int mg = 0; mg < MG; ++mg) u[qq][mat][mg] = load_coherent(prs, src + (mat * MG + mg) * 1024u);
+          for (int mg = 0; mg < MG; ++mg)
+            u[qq][mat][mg] = mine ? ow[mat][mg] : load_coherent(prs, src + (mat * MG + mg) * 1024u);
       }
 #pragma unroll
       for (int qq = 0; qq < 2; ++qq)
@@ -758,8 +771,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
 #pragma unroll
         for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
-          for (int mg = 0; mg < MG; ++mg) tot[mat][mg] += v[k][qq][mat][mg];
-    sum_rest(tl, QB, tot);
+          for (int mg = 0; mg < MG; ++mg) tot[mat][mg] += qq == q ? own[k][mat][mg] : v[k][qq][mat][mg];
+    sum_rest(tl, QB, tot, own[k]);
     gepilogue<WF, NMAT, MG>(p, g * p.G + tl, tot, ein[k], lane, th);
   }
   // tiles beyond kEpt per wave (groups of more than kEpt * NW tiles)
@@ -771,7 +784,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(GvParams p) {
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
       for (int mg = 0; mg < MG; ++mg) tot[mat][mg] = f32x4{0.f, 0.f, 0.f, 0.f};
-    sum_rest(tl, 0, tot);
+    sum_rest(tl, 0, tot, nullptr);
     gepilogue<WF, NMAT, MG>(p, g * p.G + tl, tot, e, lane, th);
   }
 }
