@@ -806,12 +806,13 @@ static size_t gemv_lds_bytes(const GemvPlan& pl, int nmat, int mg) {
 }
 
 // Work split: minimise a simple time model over the K split S.  A workgroup streams U = G * KQ
-// units (NMAT x 4352-byte blocks each); the last workgroup of a tile group then reads S * G
-// partial tiles per matrix.  Units cost ~0.16 us per matrix at a CU's share of HBM bandwidth,
-// partial tiles ~0.03 us each whatever the token groups (fitted on MI355X to the measured
-// 27B-shape splits: at 16 tokens gate/up 2 K splits beat 4, at 32 tokens 4 beat 3, and down 8
-// beat 10); splits using fewer than all CUs pay for it through their larger U.  K splits may
-// differ by one superblock.
+// units (NMAT x 4352-byte blocks each); the last workgroup of a tile group then reads the other
+// S - 1 splits' partial tiles per matrix (the model, fitted when it read all S, charges S * G).
+// Units cost ~0.16 us per matrix at a CU's share of HBM bandwidth, partial tiles ~0.03 us each
+// whatever the token groups (fitted on MI355X to the measured 27B-shape splits: at 16 tokens
+// gate/up 2 K splits beat 4, at 32 tokens 4 beat 3, and down 8 beat 10; charging S - 1 picks the
+// same splits there); splits using fewer than all CUs pay for it through their larger U.  K
+// splits may differ by one superblock.
 int plan_gemv(int rows, int K, int nmat, int mg, int num_cus, GemvPlan* out) {
   if (rows <= 0 || K <= 0 || rows % kTileRows || K % kSuperK || (mg != 1 && mg != 2) || (nmat != 1 && nmat != 2))
     return -1;
