@@ -286,3 +286,17 @@ def test_no_kernel_waits_for_another_block():
         assert not re.search(r"\bdo\s*\{", text), f"{name}: do-while loop"
         assert "s_sleep" not in text, name
     assert loops > 100
+
+
+def test_traffic_summary_matches_the_kernel_sources():
+    """bench.py puts the committed HBM counter figures in its roofline only when they were measured
+    on the current M <= 32 kernel sources; a kernel change must come with a new counter run."""
+    import importlib.util
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    spec = importlib.util.spec_from_file_location("bench_for_test", os.path.join(root, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    traffic, source = bench.read_traffic("qwen3-27b-mlp-m16-bfp8")
+    assert traffic is not None, source
+    assert traffic["gate_up"] > 189_562_880 and traffic["down"] > 94_863_360  # at least the algorithmic bytes
